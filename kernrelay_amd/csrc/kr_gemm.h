@@ -1,0 +1,34 @@
+// Host interface of the producer GEMM (see kr_gemm.hip).
+#pragma once
+
+#include "kr_common.h"
+#include "kr_relay.h"
+
+namespace kr {
+
+struct GemmDesc {
+    int dtype = kBF16;           // kBF16 or kF16 (inputs and output)
+    const void *A = nullptr;     // [M, K], row stride lda (elements)
+    const void *Bt = nullptr;    // [N, K], row stride ldb (weights, K contiguous)
+    void *C = nullptr;           // [M, N], row stride ldc
+    const void *bias = nullptr;  // optional [N]
+    int64_t lda = 0, ldb = 0, ldc = 0;
+    int M = 0, N = 0, K = 0;
+    int bm = 0;                  // M tile (0 = pick automatically)
+    int bn = 0;                  // N tile (0 = pick automatically)
+    RelayPub pub{};              // pub.ctrl == nullptr: no release
+};
+
+// Launch C = A . Bt^T (+bias). pub.rows_per_tile (when publishing) must be a
+// multiple of the chosen M tile; pub.arrivals is computed here.
+void GemmLaunch(const GemmDesc &d, hipStream_t stream);
+
+struct GemmTile {
+    int bm, bn;
+};
+
+// Tile the launcher would use for this shape ({-1,-1} when no M tile divides
+// the relay tile).
+GemmTile GemmPickTile(int M, int N, int relay_rows);
+
+}  // namespace kr

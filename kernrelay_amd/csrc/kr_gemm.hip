@@ -1,0 +1,301 @@
+// Producer GEMM: C[M,N] = A[M,K] . Bt[N,K]^T (+ bias[N]) on CDNA4 MFMA.
+//
+// Replaces the reference's aclnnMatmul producer (exec/qwen_main.cpp:499-512,
+// exec/runtime/op_impl.cpp:175-201). Weights are re-laid out once at load as
+// Bt = weight_t^T ([N,K], K contiguous) so that both operands feed
+// v_mfma_f32_32x32x16_{bf16,f16} with one 16-byte load per lane.
+//
+// * 256 threads = 4 waves in a 2x2 grid; each wave owns (BM/2)x(BN/2) of C as
+//   (BM/64)x(BN/64) 32x32 accumulator blocks (fp32, 16 values per lane).
+// * K is walked in 64-wide steps through a double-buffered LDS stage; global
+//   loads of step k+1 are in flight while step k runs on the matrix cores.
+// * LDS rows are 128 B (64 elements); the 16-byte chunk index is XOR-swizzled
+//   with (row>>1)&7 so a quarter-wave's ds_read_b128 hits distinct banks.
+// * Every variant uses the same MFMA instruction and the same K order, so a
+//   row of C is bit-identical whatever BM/BN or row range a launch covers:
+//   the split schedule is bit-exact against the unsplit one.
+// * Epilogue: acc -> 16-bit (RNE); with bias, bf16(bf16(acc)+bias) — the
+//   rounding of the reference's separate Matmul then Add (EmitQkv,
+//   exec/qwen_main.cpp:1336-1344). Then the workgroup arrives on its row
+//   tile's relay counter; the last arrival releases the tile.
+#include "kr_gemm.h"
+#include "kr_relay.h"
+
+namespace kr {
+
+namespace {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+constexpr int kBK = 64;          // K elements per LDS stage
+constexpr int kRowChunks = 8;    // 16-byte chunks per LDS row
+constexpr int kThreads = 256;
+
+struct GemmParams {
+    const uint16_t *A;
+    const uint16_t *Bt;
+    uint16_t *C;
+    const uint16_t *bias;
+    int64_t lda, ldb, ldc;
+    int M, N, K;
+    int tiles_m, tiles_n;
+    RelayPub pub;
+};
+
+__device__ __forceinline__ int Swz(int row, int chunk) { return chunk ^ ((row >> 1) & 7); }
+
+template <int DT>
+__device__ __forceinline__ f32x16 Mfma(const uint4 &a, const uint4 &b, const f32x16 &c)
+{
+    if constexpr (DT == kBF16) {
+        return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a),
+                                                       __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+    } else {
+        return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a),
+                                                      __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+    }
+}
+
+template <int DT, int BM, int BN>
+__global__ void __attribute__((amdgpu_flat_work_group_size(kThreads, kThreads),
+                               amdgpu_waves_per_eu(BM * BN >= 256 * 128 ? 1 : 2, BM * BN >= 256 * 128 ? 1 : 2)))
+GemmKernel(GemmParams p)
+{
+    constexpr int MI = BM / 64;   // 32-row blocks per wave
+    constexpr int NI = BN / 64;   // 32-col blocks per wave
+    constexpr int AL = BM * kRowChunks / kThreads;  // A chunks per thread per stage
+    constexpr int BL = BN * kRowChunks / kThreads;
+    constexpr int STAGE = (BM + BN) * kBK;           // elements per LDS stage
+
+    __shared__ __attribute__((aligned(16))) uint16_t smem[2 * STAGE];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int wm = wave >> 1;
+    const int wn = wave & 1;
+
+    // Row-tile-major order: all column blocks of a row block are dispatched
+    // together, so relay tiles complete front to back.
+    const int bid = blockIdx.x;
+    const int tm = bid / p.tiles_n;
+    const int tn = bid % p.tiles_n;
+    const int m0 = tm * BM;
+    const int n0 = tn * BN;
+
+    const int lrow = tid >> 3;       // 0..31
+    const int lchunk = tid & 7;
+
+    uint4 ra[AL], rb[BL];
+
+    auto load_global = [&](int kt) {
+        const int kc = kt * kBK + lchunk * 8;
+        const bool kin = kc < p.K;
+#pragma unroll
+        for (int j = 0; j < AL; ++j) {
+            const int r = lrow + 32 * j;
+            const int gm = m0 + r;
+            if (kin && gm < p.M) {
+                ra[j] = *reinterpret_cast<const uint4 *>(p.A + int64_t(gm) * p.lda + kc);
+            } else {
+                ra[j] = make_uint4(0, 0, 0, 0);
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < BL; ++j) {
+            const int r = lrow + 32 * j;
+            const int gn = n0 + r;
+            if (kin && gn < p.N) {
+                rb[j] = *reinterpret_cast<const uint4 *>(p.Bt + int64_t(gn) * p.ldb + kc);
+            } else {
+                rb[j] = make_uint4(0, 0, 0, 0);
+            }
+        }
+    };
+
+    auto store_lds = [&](int stage) {
+        uint16_t *As = smem + stage * STAGE;
+        uint16_t *Bs = As + BM * kBK;
+#pragma unroll
+        for (int j = 0; j < AL; ++j) {
+            const int r = lrow + 32 * j;
+            *reinterpret_cast<uint4 *>(As + r * kBK + Swz(r, lchunk) * 8) = ra[j];
+        }
+#pragma unroll
+        for (int j = 0; j < BL; ++j) {
+            const int r = lrow + 32 * j;
+            *reinterpret_cast<uint4 *>(Bs + r * kBK + Swz(r, lchunk) * 8) = rb[j];
+        }
+    };
+
+    f32x16 acc[MI][NI];
+#pragma unroll
+    for (int i = 0; i < MI; ++i)
+#pragma unroll
+        for (int j = 0; j < NI; ++j)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
+
+    const int nk = (p.K + kBK - 1) / kBK;
+    load_global(0);
+    store_lds(0);
+    __syncthreads();
+
+    const int frow = lane & 31;
+    const int fhalf = lane >> 5;
+
+    for (int kt = 0; kt < nk; ++kt) {
+        const int cur = kt & 1;
+        if (kt + 1 < nk) load_global(kt + 1);
+        const uint16_t *As = smem + cur * STAGE;
+        const uint16_t *Bs = As + BM * kBK;
+#pragma unroll
+        for (int ks = 0; ks < kBK / 16; ++ks) {
+            const int chunk = ks * 2 + fhalf;
+            uint4 fa[MI], fb[NI];
+#pragma unroll
+            for (int i = 0; i < MI; ++i) {
+                const int r = wm * (BM / 2) + i * 32 + frow;
+                fa[i] = *reinterpret_cast<const uint4 *>(As + r * kBK + Swz(r, chunk) * 8);
+            }
+#pragma unroll
+            for (int j = 0; j < NI; ++j) {
+                const int r = wn * (BN / 2) + j * 32 + frow;
+                fb[j] = *reinterpret_cast<const uint4 *>(Bs + r * kBK + Swz(r, chunk) * 8);
+            }
+#pragma unroll
+            for (int i = 0; i < MI; ++i)
+#pragma unroll
+                for (int j = 0; j < NI; ++j) acc[i][j] = Mfma<DT>(fa[i], fb[j], acc[i][j]);
+        }
+        if (kt + 1 < nk) store_lds(cur ^ 1);
+        __syncthreads();
+    }
+
+    // Epilogue. 32x32 accumulator layout: value v of lane l is
+    // row 8*(v/4) + 4*(l/32) + v%4, column l%32 of the block.
+#pragma unroll
+    for (int j = 0; j < NI; ++j) {
+        const int col = n0 + wn * (BN / 2) + j * 32 + frow;
+        if (col >= p.N) continue;
+        float bcol = 0.0f;
+        if (p.bias != nullptr) bcol = Elem<DT>::Load(p.bias[col]);
+#pragma unroll
+        for (int i = 0; i < MI; ++i) {
+#pragma unroll
+            for (int v = 0; v < 16; ++v) {
+                const int row = m0 + wm * (BM / 2) + i * 32 + 8 * (v >> 2) + 4 * fhalf + (v & 3);
+                if (row < p.M) {
+                    float x = acc[i][j][v];
+                    uint16_t o;
+                    if (p.bias != nullptr) {
+                        o = Elem<DT>::Store(RoundTo<DT>(x) + bcol);
+                    } else {
+                        o = Elem<DT>::Store(x);
+                    }
+                    p.C[int64_t(row) * p.ldc + col] = o;
+                }
+            }
+        }
+    }
+
+    if (p.pub.ctrl != nullptr) RelayArrive(p.pub, m0 / p.pub.rows_per_tile);
+}
+
+template <int DT, int BM, int BN>
+void LaunchTyped(const GemmParams &base, hipStream_t stream)
+{
+    GemmParams p = base;
+    p.tiles_m = (p.M + BM - 1) / BM;
+    p.tiles_n = (p.N + BN - 1) / BN;
+    if (p.pub.ctrl != nullptr) {
+        if (p.pub.rows_per_tile % BM != 0) throw std::runtime_error("relay tile rows not a multiple of BM");
+        p.pub.arrivals = (p.pub.rows_per_tile / BM) * p.tiles_n;
+    }
+    const dim3 grid(p.tiles_m * p.tiles_n);
+    hipLaunchKernelGGL((GemmKernel<DT, BM, BN>), grid, dim3(kThreads), 0, stream, p);
+    Check(hipGetLastError(), "gemm launch");
+}
+
+}  // namespace
+
+namespace {
+
+int Waves(int tiles, int slots) { return (tiles + slots - 1) / slots; }
+
+}  // namespace
+
+GemmTile GemmPickTile(int M, int N, int relay_rows)
+{
+    // Candidates from most to least data reuse; take the first that keeps the
+    // device busy (>= 2 full waves of workgroups) or, failing that, the one
+    // with the best wave efficiency. Every tile runs the same MFMA and K order,
+    // so the choice never changes the arithmetic.
+    static const GemmTile cands[] = {{256, 256}, {256, 128}, {128, 256}, {128, 128}, {64, 256}};
+    const int cus = 256;
+    GemmTile best{-1, -1};
+    double best_eff = -1.0;
+    for (const GemmTile &t : cands) {
+        if (relay_rows > 0 && relay_rows % t.bm != 0) continue;
+        const int tiles = ((M + t.bm - 1) / t.bm) * ((N + t.bn - 1) / t.bn);
+        const int slots = cus * (t.bm * t.bn >= 256 * 128 ? 1 : 2);
+        if (tiles >= 2 * slots) return t;
+        const double work = double(t.bm) * t.bn;  // per-workgroup work unit
+        const double eff = double(tiles) * work / (double(Waves(tiles, slots)) * slots * work);
+        const double score = eff * (t.bm * t.bn >= 256 * 128 ? 1.0 : 0.85);
+        if (score > best_eff) {
+            best_eff = score;
+            best = t;
+        }
+    }
+    return best;
+}
+
+void GemmLaunch(const GemmDesc &d, hipStream_t stream)
+{
+    if (d.K % 8 != 0) throw std::runtime_error("gemm: K must be a multiple of 8");
+    if (d.M <= 0 || d.N <= 0 || d.K <= 0) throw std::runtime_error("gemm: empty shape");
+    if ((reinterpret_cast<uintptr_t>(d.A) | reinterpret_cast<uintptr_t>(d.Bt)) & 15)
+        throw std::runtime_error("gemm: A/Bt must be 16-byte aligned");
+    if ((d.lda | d.ldb) % 8 != 0) throw std::runtime_error("gemm: lda/ldb must be multiples of 8");
+    GemmParams p{};
+    p.A = static_cast<const uint16_t *>(d.A);
+    p.Bt = static_cast<const uint16_t *>(d.Bt);
+    p.C = static_cast<uint16_t *>(d.C);
+    p.bias = static_cast<const uint16_t *>(d.bias);
+    p.lda = d.lda;
+    p.ldb = d.ldb;
+    p.ldc = d.ldc;
+    p.M = d.M;
+    p.N = d.N;
+    p.K = d.K;
+    p.pub = d.pub;
+    const int relay_rows = d.pub.ctrl != nullptr ? d.pub.rows_per_tile : 0;
+    GemmTile t = GemmPickTile(d.M, d.N, relay_rows);
+    if (d.bm > 0) {
+        // a forced M tile pairs with the widest N tile built for it
+        t.bm = d.bm;
+        t.bn = d.bn > 0 ? d.bn : 256;
+    } else if (d.bn > 0) {
+        t.bn = d.bn;
+    }
+    if (t.bm < 0) throw std::runtime_error("gemm: relay tile rows must be a multiple of 64");
+    const bool bf = d.dtype == kBF16;
+    if (d.dtype != kBF16 && d.dtype != kF16) throw std::runtime_error("gemm: dtype must be bf16 or f16");
+#define KR_GEMM_CASE(BM_, BN_)                                                                     \
+    if (t.bm == BM_ && t.bn == BN_) {                                                              \
+        bf ? LaunchTyped<kBF16, BM_, BN_>(p, stream) : LaunchTyped<kF16, BM_, BN_>(p, stream);    \
+        return;                                                                                    \
+    }
+    KR_GEMM_CASE(256, 256)
+    KR_GEMM_CASE(256, 128)
+    KR_GEMM_CASE(128, 256)
+    KR_GEMM_CASE(128, 128)
+    KR_GEMM_CASE(64, 256)
+#undef KR_GEMM_CASE
+    throw std::runtime_error("gemm: unsupported tile " + std::to_string(t.bm) + "x" + std::to_string(t.bn));
+}
+
+}  // namespace kr

@@ -1,0 +1,176 @@
+// C ABI of the op-level kernels (include/kr_ops.h).
+#include "../../include/kr_ops.h"
+
+#include <string>
+
+#include "kr_gemm.h"
+#include "kr_misc.h"
+#include "kr_rowops.h"
+
+static_assert(sizeof(kr_wait) == sizeof(kr::RelayWait), "kr_wait layout");
+static_assert(offsetof(kr_wait, max_spins) == offsetof(kr::RelayWait, max_spins), "kr_wait layout");
+static_assert(sizeof(kr_pub) == sizeof(kr::RelayPub), "kr_pub layout");
+static_assert(offsetof(kr_pub, arrivals) == offsetof(kr::RelayPub, arrivals), "kr_pub layout");
+
+namespace {
+
+thread_local std::string g_last_error;
+
+template <typename F>
+int Guard(F &&f)
+{
+    try {
+        g_last_error.clear();
+        f();
+        return 0;
+    } catch (const std::exception &e) {
+        g_last_error = e.what();
+        return 1;
+    }
+}
+
+kr::RelayWait ToWait(const kr_wait *w)
+{
+    kr::RelayWait r{};
+    if (w == nullptr || w->ctrl == nullptr) return r;
+    r.ctrl = w->ctrl;
+    r.flag0 = w->flag0;
+    r.state0 = w->state0;
+    r.prod_rows = w->prod_rows;
+    r.row_off = w->row_off;
+    r.adv_lo = w->adv_lo;
+    r.adv_hi = w->adv_hi;
+    r.max_spins = w->max_spins ? w->max_spins : kr::kDefaultMaxSpins;
+    if (r.prod_rows <= 0) throw std::runtime_error("wait: prod_rows must be > 0");
+    if (r.row_off < 0) throw std::runtime_error("wait: row_off must be >= 0");
+    return r;
+}
+
+kr::RelayPub ToPub(const kr_pub *p)
+{
+    kr::RelayPub r{};
+    if (p == nullptr || p->ctrl == nullptr) return r;
+    r.ctrl = p->ctrl;
+    r.flag0 = p->flag0;
+    r.rows_per_tile = p->rows_per_tile;
+    if (r.rows_per_tile <= 0) throw std::runtime_error("pub: rows_per_tile must be > 0");
+    return r;
+}
+
+hipStream_t S(void *s) { return static_cast<hipStream_t>(s); }
+
+}  // namespace
+
+extern "C" {
+
+const char *kr_ops_last_error(void) { return g_last_error.c_str(); }
+
+int kr_op_gemm(int dtype, const void *A, int64_t lda, const void *Bt, int64_t ldb, void *C, int64_t ldc,
+               const void *bias, int M, int N, int K, int bm, const kr_pub *pub, void *stream)
+{
+    return Guard([&] {
+        kr::GemmDesc d;
+        d.dtype = dtype;
+        d.A = A;
+        d.Bt = Bt;
+        d.C = C;
+        d.bias = bias;
+        d.lda = lda;
+        d.ldb = ldb;
+        d.ldc = ldc;
+        d.M = M;
+        d.N = N;
+        d.K = K;
+        d.bm = bm;
+        d.pub = ToPub(pub);
+        if (d.pub.ctrl && M % d.pub.rows_per_tile != 0) throw std::runtime_error("gemm: M must be a multiple of rows_per_tile");
+        kr::GemmLaunch(d, S(stream));
+    });
+}
+
+int kr_op_elementwise(int op, int dtype_in, int dtype_out, const void *x0, const void *x1, void *y, int rows,
+                      int cols, int tile_rows, int grid, const kr_wait *wait, const kr_pub *pub, void *stream)
+{
+    return Guard([&] {
+        kr::EwDesc d;
+        d.op = op;
+        d.dtype_in = dtype_in;
+        d.dtype_out = dtype_out;
+        d.x0 = x0;
+        d.x1 = x1;
+        d.y = y;
+        d.rows = rows;
+        d.cols = cols;
+        d.tile_rows = tile_rows;
+        d.grid = grid;
+        d.wait = ToWait(wait);
+        d.pub = ToPub(pub);
+        kr::EwLaunch(d, S(stream));
+        kr::Check(hipGetLastError(), "elementwise launch");
+    });
+}
+
+int kr_op_rowop(int op, int dtype, const void *x0, const void *x1, const void *gamma, void *y, void *sum_out,
+                float *rstd_out, int rows, int cols, float eps, int tile_rows, int grid, const kr_wait *wait,
+                const kr_pub *pub, void *stream)
+{
+    return Guard([&] {
+        kr::RowDesc d;
+        d.op = op;
+        d.dtype = dtype;
+        d.x0 = x0;
+        d.x1 = x1;
+        d.gamma = gamma;
+        d.y = y;
+        d.sum_out = sum_out;
+        d.rstd_out = rstd_out;
+        d.rows = rows;
+        d.cols = cols;
+        d.eps = eps;
+        d.tile_rows = tile_rows;
+        d.grid = grid;
+        d.wait = ToWait(wait);
+        d.pub = ToPub(pub);
+        kr::RowLaunch(d, S(stream));
+        kr::Check(hipGetLastError(), "row op launch");
+    });
+}
+
+int kr_op_wait(const kr_wait *wait, int lo, int hi, void *stream)
+{
+    return Guard([&] { kr::WaitLaunch(ToWait(wait), lo, hi, S(stream)); });
+}
+
+int kr_op_publish(const kr_pub *pub, int tile, void *stream)
+{
+    return Guard([&] {
+        kr::RelayPub p = ToPub(pub);
+        if (p.ctrl && pub->rows_per_tile <= 0) throw std::runtime_error("publish: bad tile");
+        kr::PublishLaunch(p, tile, S(stream));
+    });
+}
+
+int kr_op_embedding(const void *table, const int64_t *ids, void *out, int rows, int cols, int64_t vocab,
+                    void *stream)
+{
+    return Guard([&] { kr::EmbedLaunch(table, ids, out, rows, cols, vocab, S(stream)); });
+}
+
+int kr_op_rope(int dtype, void *x, int64_t ld, int S_, int heads, int D, const void *cos_t, const void *sin_t,
+               void *stream)
+{
+    return Guard([&] { kr::RopeLaunch(dtype, x, ld, S_, heads, D, cos_t, sin_t, S(stream)); });
+}
+
+int kr_op_attention(int dtype, const void *q, int64_t ldq, const void *k, int64_t ldk, const void *v, int64_t ldv,
+                    void *out, int64_t ldo, int S_, int HQ, int HKV, int D, float scale, void *stream)
+{
+    return Guard([&] { kr::AttnLaunch(dtype, q, ldq, k, ldk, v, ldv, out, ldo, S_, HQ, HKV, D, scale, S(stream)); });
+}
+
+int kr_op_transpose(const void *src, void *dst, int R, int C, void *stream)
+{
+    return Guard([&] { kr::TransposeLaunch(src, dst, R, C, S(stream)); });
+}
+
+}  // extern "C"

@@ -1,0 +1,953 @@
+// Schedule executor behind kr_plan_run: the MI355X counterpart of the
+// reference's nhp_exec (exec/exec_main.cpp:1325-1494).
+//
+// A schedule.json lists nodes (op, rows/cols/k/n, tiles) and, per engine
+// stream, the ordered (node, tile) tasks with their cross-stream waits and
+// publish marks plus explicit row geometry (in_row_off, in_rows,
+// out_row_off). Engines map onto two HIP streams: "aic" (matrix work) on the
+// producer stream, "aiv" (vector work) on the consumer stream; a schedule
+// that also holds MIX ("aicore") tasks is merged into one stream in global
+// topological order, as the reference does (NormalizeTopology,
+// exec_main.cpp:243-341).
+//
+// Cross-stream dependencies are device flags by default (KR_SYNC=flag):
+// a publishing task releases its tile from its own epilogue, and a waiting
+// task either spins in its own prologue (row/elementwise consumers, one
+// producer node, contiguous tiles) or behind a one-workgroup wait kernel.
+// KR_SYNC=event uses hipEvents instead (the reference's default,
+// exec_main.cpp:700-723).
+//
+// Inputs follow the reference convention (DetValue/NodeSeed, seeds +1 input,
+// +2 weight, +3 second operand: exec_main.cpp:498-540) unless a node names
+// input files ("inputs": {"in","b","x1","gamma"}). The checksum is the
+// reference's: sum over ranks and nodes of the first 8192 16-bit outputs
+// (exec_main.cpp:1292-1311).
+#include <algorithm>
+#include <cstdio>
+#include <fstream>
+#include <map>
+#include <memory>
+#include <numeric>
+#include <set>
+#include <tuple>
+#include <sstream>
+
+#include "kr_gemm.h"
+#include "kr_json.h"
+#include "kr_misc.h"
+#include "kr_rowops.h"
+#include "kr_runtime.h"
+
+namespace kr {
+namespace plan {
+
+using json::Value;
+
+enum class Op { MatMul, Gelu, Softmax, Cast, Add, Silu, Mul, Swiglu, RmsNorm, AddRmsNorm };
+
+Op ParseOp(const std::string &s)
+{
+    if (s == "matmul") return Op::MatMul;
+    if (s == "gelu") return Op::Gelu;
+    if (s == "softmax") return Op::Softmax;
+    if (s == "cast") return Op::Cast;
+    if (s == "add") return Op::Add;
+    if (s == "silu") return Op::Silu;
+    if (s == "mul") return Op::Mul;
+    if (s == "swiglu") return Op::Swiglu;
+    if (s == "rmsnorm") return Op::RmsNorm;
+    if (s == "add_rmsnorm") return Op::AddRmsNorm;
+    throw std::runtime_error("op '" + s + "' is not built on this target "
+                             "(supported: matmul gelu softmax cast add silu mul swiglu rmsnorm add_rmsnorm)");
+}
+
+int ParseDType(const std::string &s)
+{
+    if (s.empty() || s == "fp16" || s == "float16" || s == "f16") return kF16;
+    if (s == "bf16" || s == "bfloat16") return kBF16;
+    if (s == "fp32" || s == "float32" || s == "f32") return kF32;
+    throw std::runtime_error("unknown dtype '" + s + "'");
+}
+
+bool IsBinary(Op op) { return op == Op::Add || op == Op::Mul || op == Op::Swiglu || op == Op::AddRmsNorm; }
+
+struct NodeSpec {
+    std::string id;
+    Op op = Op::Add;
+    std::string opname;
+    std::string engine;
+    int dtype = kF16;
+    int out_dtype = kF16;
+    int64_t rows = 0, cols = 0, k = 0, n = 0;
+    int tiles = 1;
+    bool split = false;
+    float eps = 1e-6f;
+    std::vector<std::string> preds;
+    std::map<std::string, std::string> inputs;
+};
+
+struct TaskSpec {
+    std::string node;
+    int tile = 0;
+    std::vector<std::pair<std::string, int>> waits;
+    bool publish = false;
+    bool has_geom = false;
+    int64_t in_row_off = 0, in_rows = 0, out_row_off = 0;
+    int64_t n_off = 0, n_tile = 0;
+};
+
+struct Lane {
+    std::string engine;
+    std::vector<TaskSpec> tasks;
+};
+
+struct SchedDoc {
+    std::string dag, group;
+    int nranks = 1;
+    std::vector<NodeSpec> nodes;
+    std::map<std::string, size_t> index;
+    std::vector<Lane> lanes;  // in engine order
+
+    const NodeSpec &Node(const std::string &id) const
+    {
+        auto it = index.find(id);
+        if (it == index.end()) throw std::runtime_error("missing plan for task: unknown node " + id);
+        return nodes[it->second];
+    }
+};
+
+int EngineRank(const std::string &e)
+{
+    if (e == "aicore" || e == "compute") return 0;
+    if (e == "aic") return 1;
+    if (e == "aiv") return 2;
+    if (e == "aicpu") return 3;
+    if (e == "hccl") return 4;
+    throw std::runtime_error("unknown engine " + e);
+}
+
+SchedDoc ParseSchedule(const Value &root)
+{
+    SchedDoc doc;
+    doc.dag = root.Str("dag");
+    doc.group = root.Str("group");
+    doc.nranks = std::max(1, int(root.Num("nranks", 1)));
+    for (const auto &n : root.At("nodes").Items()) {
+        NodeSpec s;
+        s.id = n.Str("id");
+        s.opname = n.Str("op");
+        s.op = ParseOp(s.opname);
+        s.engine = n.Str("engine", "aiv");
+        s.dtype = ParseDType(n.Str("dtype", "fp16"));
+        if (s.dtype == kF32) throw std::runtime_error("node " + s.id + ": fp32 inputs are not supported");
+        s.rows = int64_t(n.Num("rows"));
+        s.cols = int64_t(n.Num("cols"));
+        s.k = int64_t(n.Num("k"));
+        s.n = int64_t(n.Num("n"));
+        s.tiles = std::max(1, int(n.Num("tiles", 1)));
+        s.split = n.Flag("split", false);
+        s.eps = float(n.Num("eps", 1e-6));
+        if (n.Has("preds"))
+            for (const auto &p : n.At("preds").Items()) s.preds.push_back(p.AsString());
+        if (n.Has("inputs"))
+            for (const auto &kv : n.At("inputs").Members()) s.inputs[kv.first] = kv.second.AsString();
+        if (s.op == Op::Cast) {
+            const std::string to = n.Str("to", "");
+            s.out_dtype = !to.empty() ? ParseDType(to) : (s.dtype == kF16 ? kF32 : kF16);
+        } else {
+            s.out_dtype = s.dtype;
+        }
+        if (s.rows <= 0 || s.cols <= 0) throw std::runtime_error("node " + s.id + ": rows/cols must be > 0");
+        if (s.op == Op::MatMul && (s.k <= 0 || s.n <= 0 || s.n != s.cols))
+            throw std::runtime_error("node " + s.id + ": matmul needs k > 0 and n == cols");
+        if (doc.index.count(s.id)) throw std::runtime_error("duplicate node id " + s.id);
+        doc.index[s.id] = doc.nodes.size();
+        doc.nodes.push_back(s);
+    }
+    std::map<std::string, Lane> by_engine;
+    for (const auto &kv : root.At("streams").Members()) {
+        const std::string name = kv.first == "compute" ? "aicore" : kv.first;
+        (void)EngineRank(name);
+        if (by_engine.count(name)) throw std::runtime_error("duplicate engine stream " + name);
+        Lane lane;
+        lane.engine = name;
+        for (const auto &t : kv.second.Items()) {
+            TaskSpec task;
+            task.node = t.Str("node");
+            task.tile = int(t.Num("tile", 0));
+            task.publish = t.Flag("publish", false);
+            if (t.Has("wait"))
+                for (const auto &w : t.At("wait").Items())
+                    task.waits.emplace_back(w.At(size_t(0)).AsString(), int(w.At(size_t(1)).AsNumber()));
+            if (t.Has("in_row_off") && t.Has("in_rows")) {
+                task.has_geom = true;
+                task.in_row_off = int64_t(t.Num("in_row_off"));
+                task.in_rows = int64_t(t.Num("in_rows"));
+                task.out_row_off = t.Has("out_row_off") ? int64_t(t.Num("out_row_off")) : task.in_row_off;
+                task.n_off = int64_t(t.Num("n_off", 0));
+                task.n_tile = int64_t(t.Num("n_tiles", 0));
+            }
+            lane.tasks.push_back(task);
+        }
+        by_engine[name] = std::move(lane);
+    }
+    for (auto &kv : by_engine) doc.lanes.push_back(std::move(kv.second));
+    std::sort(doc.lanes.begin(), doc.lanes.end(),
+              [](const Lane &a, const Lane &b) { return EngineRank(a.engine) < EngineRank(b.engine); });
+    return doc;
+}
+
+using Key = std::pair<std::string, int>;
+
+// Global topological order over all tasks (hard edges: same-lane FIFO and
+// every wait); ties broken by (engine rank, lane position).
+std::vector<std::pair<size_t, size_t>> TopoOrder(const SchedDoc &doc)
+{
+    std::map<Key, std::pair<size_t, size_t>> pos;
+    std::vector<std::pair<size_t, size_t>> keys;
+    for (size_t l = 0; l < doc.lanes.size(); ++l)
+        for (size_t i = 0; i < doc.lanes[l].tasks.size(); ++i) {
+            const auto &t = doc.lanes[l].tasks[i];
+            const Key k{t.node, t.tile};
+            if (pos.count(k)) throw std::runtime_error("duplicate task for node " + t.node + " tile " + std::to_string(t.tile));
+            pos[k] = {l, i};
+            keys.emplace_back(l, i);
+        }
+    std::map<std::pair<size_t, size_t>, std::set<std::pair<size_t, size_t>>> deps;
+    for (const auto &key : keys) {
+        std::set<std::pair<size_t, size_t>> d;
+        if (key.second > 0) d.insert({key.first, key.second - 1});
+        for (const auto &w : doc.lanes[key.first].tasks[key.second].waits) {
+            auto it = pos.find(w);
+            if (it == pos.end()) throw std::runtime_error("wait on unpublished flag " + w.first + "#" + std::to_string(w.second));
+            if (it->second != key) d.insert(it->second);
+        }
+        deps[key] = std::move(d);
+    }
+    auto rank = [&](const std::pair<size_t, size_t> &k) {
+        return std::make_pair(EngineRank(doc.lanes[k.first].engine), k.second);
+    };
+    std::vector<std::pair<size_t, size_t>> order, ready;
+    for (const auto &k : keys)
+        if (deps[k].empty()) ready.push_back(k);
+    std::set<std::pair<size_t, size_t>> done;
+    while (!ready.empty()) {
+        auto it = std::min_element(ready.begin(), ready.end(), [&](const auto &a, const auto &b) { return rank(a) < rank(b); });
+        const auto cur = *it;
+        ready.erase(it);
+        order.push_back(cur);
+        done.insert(cur);
+        for (auto &kv : deps) {
+            if (done.count(kv.first) || !kv.second.count(cur)) continue;
+            kv.second.erase(cur);
+            if (kv.second.empty()) ready.push_back(kv.first);
+        }
+    }
+    if (order.size() != keys.size()) throw std::runtime_error("schedule contains wait cycle");
+    return order;
+}
+
+// MIX (aicore) tasks may not overlap pure aic/aiv work: merge those lanes into
+// one in global topological order (exec_main.cpp:243-341).
+void NormalizeTopology(SchedDoc &doc)
+{
+    auto order = TopoOrder(doc);
+    bool has_mix = false, has_pure = false;
+    for (const auto &l : doc.lanes) {
+        if (l.tasks.empty()) continue;
+        if (l.engine == "aicore") has_mix = true;
+        if (l.engine == "aic" || l.engine == "aiv") has_pure = true;
+    }
+    for (const auto &l : doc.lanes)
+        if (!l.tasks.empty() && (l.engine == "aicpu" || l.engine == "hccl"))
+            throw std::runtime_error("engine " + l.engine + " has no executor on this target");
+    if (!(has_mix && has_pure)) {
+        std::vector<Lane> keep;
+        for (auto &l : doc.lanes)
+            if (!l.tasks.empty()) keep.push_back(std::move(l));
+        doc.lanes = std::move(keep);
+        return;
+    }
+    Lane merged;
+    merged.engine = "aicore";
+    for (const auto &k : order) merged.tasks.push_back(doc.lanes[k.first].tasks[k.second]);
+    doc.lanes.clear();
+    doc.lanes.push_back(std::move(merged));
+}
+
+// ------------------------------------------------------------------ runtime
+struct NodeBuf {
+    DevBuf out, bt, own_in, aux, gamma, sum;
+    size_t out_bytes = 0;
+};
+
+struct Launch {
+    int lane = 0;
+    const TaskSpec *task = nullptr;
+    const NodeSpec *node = nullptr;
+    // relay wiring
+    bool fused_wait = false;
+    RelayWait wait{};
+    int tile_rows = 0;
+    std::vector<RelayWait> extra_waits;  // standalone one-workgroup waits
+    bool publish = false;
+    int flag = -1;
+    hipEvent_t pub_event = nullptr;
+    std::vector<hipEvent_t> wait_events;
+};
+
+struct RankCtx {
+    int rank = 0;
+    std::map<std::string, NodeBuf> bufs;
+};
+
+class Executor {
+public:
+    Executor(SchedDoc doc, int device, std::string mode)
+        : doc_(std::move(doc)), device_(device), mode_(std::move(mode))
+    {
+        sync_ = EnvStr("KR_SYNC", "flag");
+        if (sync_ != "flag" && sync_ != "event") throw std::runtime_error("KR_SYNC must be flag or event");
+        wait_kind_ = EnvStr("KR_RELAY_WAIT", "fused");
+        relay_grid_ = EnvInt("KR_RELAY_GRID", 64);
+        max_spins_ = uint32_t(EnvInt("KR_MAX_SPINS", int(kDefaultMaxSpins)));
+        if (mode_ != "direct" && mode_ != "graph" && mode_ != "graph_per_stream")
+            throw std::runtime_error("mode '" + mode_ + "' is not built (direct, graph, graph_per_stream)");
+    }
+
+    ~Executor()
+    {
+        for (auto &g : graphs_) {
+            if (g.exec) (void)hipGraphExecDestroy(g.exec);
+            if (g.graph) (void)hipGraphDestroy(g.graph);
+        }
+        for (auto &L : launches_) {
+            if (L.pub_event) (void)hipEventDestroy(L.pub_event);
+        }
+        if (ev0_) (void)hipEventDestroy(ev0_);
+        if (ev1_) (void)hipEventDestroy(ev1_);
+        if (ev2_) (void)hipEventDestroy(ev2_);
+        streams_.Destroy();
+    }
+
+    // Host-only checks: every rejection happens before the device is touched.
+    void Validate() { ValidateGeometry(); }
+
+    void Prepare()
+    {
+        ValidateGeometry();
+        Check(hipSetDevice(device_), "hipSetDevice");
+        streams_.Create(device_);
+        Check(hipEventCreate(&ev0_), "event");
+        Check(hipEventCreate(&ev1_), "event");
+        Check(hipEventCreate(&ev2_), "event");
+        ranks_.resize(doc_.nranks);
+        for (int r = 0; r < doc_.nranks; ++r) {
+            ranks_[r].rank = r;
+            for (const auto &n : doc_.nodes) Allocate(ranks_[r], n);
+            Upload(ranks_[r]);
+        }
+        Wire();
+        Check(hipDeviceSynchronize(), "prepare sync");
+        if (mode_ != "direct") Capture();
+    }
+
+    // One execution of every rank's program; returns the makespan (max over
+    // ranks, ranks run back to back on the one device) in microseconds.
+    double RunOnce(double *dev_us)
+    {
+        double makespan = 0.0, dev = 0.0;
+        for (int r = 0; r < doc_.nranks; ++r) {
+            Check(hipDeviceSynchronize(), "pre-run sync");
+            const auto t0 = Clock::now();
+            Check(hipEventRecord(ev0_, streams_.prod), "record start");
+            Check(hipStreamWaitEvent(streams_.cons, ev0_, 0), "consumer start");
+            if (mode_ == "direct") {
+                EnqueueRank(r);
+            } else {
+                for (auto &g : graphs_)
+                    if (g.rank == r) Check(hipGraphLaunch(g.exec, g.lane == 0 ? streams_.prod : streams_.cons), "graph launch");
+            }
+            Check(hipEventRecord(ev1_, streams_.prod), "record end prod");
+            Check(hipEventRecord(ev2_, streams_.cons), "record end cons");
+            Check(hipStreamSynchronize(streams_.prod), "sync prod");
+            Check(hipStreamSynchronize(streams_.cons), "sync cons");
+            const auto t1 = Clock::now();
+            float a = 0.f, b = 0.f;
+            Check(hipEventElapsedTime(&a, ev0_, ev1_), "elapsed");
+            Check(hipEventElapsedTime(&b, ev0_, ev2_), "elapsed");
+            makespan = std::max(makespan, Us(t0, t1));
+            dev = std::max(dev, 1000.0 * std::max(a, b));
+        }
+        if (dev_us) *dev_us = dev;
+        return makespan;
+    }
+
+    int FlagTimeouts()
+    {
+        if (ctrl_words_ == 0) return 0;
+        std::vector<int32_t> host(ctrl_words_);
+        Check(hipMemcpy(host.data(), ctrl_.get(), ctrl_words_ * 4, hipMemcpyDeviceToHost), "ctrl d2h");
+        int bad = 0;
+        for (int s : consumed_states_)
+            if (host[size_t(s) * kWords + kOffStatus] != 1) ++bad;
+        return bad;
+    }
+
+    double Checksum()
+    {
+        double sum = 0.0;
+        for (auto &rc : ranks_)
+            for (const auto &n : doc_.nodes) {
+                const NodeBuf &b = rc.bufs.at(n.id);
+                const size_t elems = std::min<size_t>(b.out_bytes / 2, 8192);
+                std::vector<uint16_t> host(elems);
+                Check(hipMemcpy(host.data(), b.out.get(), elems * 2, hipMemcpyDeviceToHost), "checksum d2h");
+                // 16-bit words are read in the output's 16-bit format; an fp32
+                // output is read as fp16 halves, exactly as the reference does.
+                const bool bf = n.out_dtype == kBF16;
+                for (uint16_t h : host) sum += double(bf ? HostBF16ToF32(h) : HostF16ToF32(h));
+            }
+        return sum;
+    }
+
+    void Dump(const std::string &dir)
+    {
+        for (const auto &n : doc_.nodes) {
+            const NodeBuf &b = ranks_[0].bufs.at(n.id);
+            std::vector<char> host(b.out_bytes);
+            Check(hipMemcpy(host.data(), b.out.get(), b.out_bytes, hipMemcpyDeviceToHost), "dump d2h");
+            std::ofstream f(dir + "/" + n.id + ".bin", std::ios::binary);
+            f.write(host.data(), std::streamsize(host.size()));
+        }
+    }
+
+    const SchedDoc &doc() const { return doc_; }
+    int edges() const { return int(consumed_states_.size()); }
+    const std::string &sync() const { return sync_; }
+    int consumer_cus() const { return streams_.cons_cus; }
+
+private:
+    int64_t OutRows(const NodeSpec &n) const { return n.rows; }
+    int64_t InCols(const NodeSpec &n) const { return n.op == Op::MatMul ? n.k : n.cols; }
+
+    void ValidateGeometry()
+    {
+        for (const auto &lane : doc_.lanes)
+            for (const auto &t : lane.tasks) {
+                const NodeSpec &n = doc_.Node(t.node);
+                const int tiles = n.split ? n.tiles : 1;
+                if (t.tile < 0 || t.tile >= tiles)
+                    throw std::runtime_error("missing plan for task " + t.node + "#" + std::to_string(t.tile));
+                const int64_t rt = n.rows / tiles;
+                const int64_t in_off = t.has_geom ? t.in_row_off : t.tile * rt;
+                const int64_t in_rows = t.has_geom ? t.in_rows : rt;
+                const int64_t out_off = t.has_geom ? t.out_row_off : t.tile * rt;
+                const int64_t limit = n.preds.empty() ? n.rows : OutRows(doc_.Node(n.preds[0]));
+                if (in_off < 0 || in_rows <= 0 || in_off + in_rows > limit)
+                    throw std::runtime_error("task " + t.node + "#" + std::to_string(t.tile) + " input rows [" +
+                                             std::to_string(in_off) + "," + std::to_string(in_off + in_rows) +
+                                             ") exceed " + std::to_string(limit));
+                if (out_off < 0 || out_off + in_rows > OutRows(n))
+                    throw std::runtime_error("task " + t.node + "#" + std::to_string(t.tile) + " output rows exceed " +
+                                             std::to_string(OutRows(n)));
+                if (t.n_tile > 0 && (t.n_off < 0 || t.n_off + t.n_tile > n.n))
+                    throw std::runtime_error("task " + t.node + "#" + std::to_string(t.tile) + " N tile exceed " +
+                                             std::to_string(n.n));
+            }
+        std::set<Key> publishing;
+        for (const auto &lane : doc_.lanes)
+            for (const auto &t : lane.tasks)
+                if (t.publish) publishing.insert({t.node, t.tile});
+        for (const auto &lane : doc_.lanes)
+            for (const auto &t : lane.tasks)
+                for (const auto &w : t.waits)
+                    if (!publishing.count(w))
+                        throw std::runtime_error("wait on unpublished flag " + w.first + "#" + std::to_string(w.second));
+        (void)TopoOrder(doc_);
+    }
+
+    std::vector<uint16_t> HostInput(const NodeSpec &n, const std::string &role, size_t elems, uint32_t seed, int dtype)
+    {
+        std::vector<uint16_t> host(elems);
+        auto it = n.inputs.find(role);
+        if (it != n.inputs.end()) {
+            std::ifstream f(it->second, std::ios::binary | std::ios::ate);
+            if (!f) throw std::runtime_error("node " + n.id + ": cannot open input " + it->second);
+            const size_t bytes = size_t(f.tellg());
+            if (bytes != elems * 2)
+                throw std::runtime_error("node " + n.id + ": input " + role + " has " + std::to_string(bytes) +
+                                         " bytes, expected " + std::to_string(elems * 2));
+            f.seekg(0);
+            f.read(reinterpret_cast<char *>(host.data()), std::streamsize(bytes));
+            return host;
+        }
+        for (size_t i = 0; i < elems; ++i) {
+            const float v = DetValue(seed, i);
+            host[i] = dtype == kBF16 ? HostF32ToBF16(v) : HostF32ToF16(v);
+        }
+        return host;
+    }
+
+    void Allocate(RankCtx &rc, const NodeSpec &n)
+    {
+        NodeBuf b;
+        b.out_bytes = size_t(n.rows) * n.cols * DTypeBytes(n.out_dtype);
+        b.out.Alloc(b.out_bytes);
+        Check(hipMemset(b.out.get(), 0, b.out_bytes), "memset out");
+        const size_t rows = size_t(n.rows), cols = size_t(n.cols);
+        if (n.preds.empty()) b.own_in.Alloc(rows * InCols(n) * 2);
+        if (n.op == Op::MatMul) b.bt.Alloc(size_t(n.k) * n.n * 2);
+        if (IsBinary(n.op) && n.preds.size() < 2) b.aux.Alloc(rows * cols * 2);
+        if (n.op == Op::RmsNorm || n.op == Op::AddRmsNorm) b.gamma.Alloc(cols * 2);
+        if (n.op == Op::AddRmsNorm) b.sum.Alloc(rows * cols * 2);
+        rc.bufs[n.id] = std::move(b);
+    }
+
+    void Upload(RankCtx &rc)
+    {
+        for (const auto &n : doc_.nodes) {
+            NodeBuf &b = rc.bufs[n.id];
+            const uint32_t seed = NodeSeed(n.id, uint32_t(rc.rank));
+            const size_t rows = size_t(n.rows), cols = size_t(n.cols);
+            if (b.own_in.get()) {
+                auto h = HostInput(n, "in", rows * InCols(n), seed + 1, n.dtype);
+                Check(hipMemcpy(b.own_in.get(), h.data(), h.size() * 2, hipMemcpyHostToDevice), "upload in");
+            }
+            if (n.op == Op::MatMul) {
+                // weight generated / read as [K, N] (the reference's layout),
+                // re-laid out once to [N, K] for the MFMA kernel.
+                auto h = HostInput(n, "b", size_t(n.k) * n.n, seed + 2, n.dtype);
+                DevBuf stage(h.size() * 2);
+                Check(hipMemcpy(stage.get(), h.data(), h.size() * 2, hipMemcpyHostToDevice), "upload b");
+                TransposeLaunch(stage.get(), b.bt.get(), int(n.k), int(n.n), nullptr);
+                Check(hipDeviceSynchronize(), "transpose sync");
+            }
+            if (b.gamma.get()) {
+                auto h = HostInput(n, "gamma", cols, seed + 2, n.dtype);
+                Check(hipMemcpy(b.gamma.get(), h.data(), h.size() * 2, hipMemcpyHostToDevice), "upload gamma");
+            }
+            if (b.aux.get()) {
+                auto h = HostInput(n, "x1", rows * cols, seed + 3, n.dtype);
+                Check(hipMemcpy(b.aux.get(), h.data(), h.size() * 2, hipMemcpyHostToDevice), "upload x1");
+            }
+        }
+    }
+
+    int LaneOf(const std::string &engine) const
+    {
+        // lane 0 = producer stream, lane 1 = consumer stream
+        if (doc_.lanes.size() == 1) return 0;
+        return engine == "aiv" ? 1 : 0;
+    }
+
+    int NodeTiles(const NodeSpec &n) const { return n.split ? n.tiles : 1; }
+
+    void Wire()
+    {
+        // launches in per-lane order
+        std::map<Key, size_t> launch_of;
+        for (size_t l = 0; l < doc_.lanes.size(); ++l)
+            for (const auto &t : doc_.lanes[l].tasks) {
+                Launch L;
+                L.lane = LaneOf(doc_.lanes[l].engine);
+                L.task = &t;
+                L.node = &doc_.Node(t.node);
+                L.publish = t.publish;
+                launch_of[{t.node, t.tile}] = launches_.size();
+                launches_.push_back(L);
+            }
+        if (doc_.lanes.size() > 2) throw std::runtime_error("more than two engine lanes after normalization");
+        // Which tasks are awaited: only cross-lane waits need a flag/event.
+        std::map<std::string, int> flag_base;
+        int next_block = 0;
+        for (const auto &n : doc_.nodes) {
+            flag_base[n.id] = next_block;
+            next_block += NodeTiles(n);
+        }
+        // state blocks per (consumer node, producer node)
+        std::map<std::pair<std::string, std::string>, int> state_base;
+        // last waiter per (consumer node, producer node, producer tile)
+        std::map<std::tuple<std::string, std::string, int>, size_t> last_waiter;
+        for (size_t i = 0; i < launches_.size(); ++i) {
+            Launch &L = launches_[i];
+            for (const auto &w : L.task->waits) {
+                auto it = launch_of.find(w);
+                if (it == launch_of.end()) throw std::runtime_error("missing plan for task " + w.first);
+                const Launch &P = launches_[it->second];
+                if (!P.task->publish) throw std::runtime_error("wait on unpublished flag " + w.first + "#" + std::to_string(w.second));
+                const auto sk = std::make_pair(L.node->id, w.first);
+                if (!state_base.count(sk)) {
+                    state_base[sk] = next_block;
+                    next_block += NodeTiles(doc_.Node(w.first));
+                }
+                last_waiter[std::make_tuple(L.node->id, w.first, w.second)] = i;
+            }
+        }
+        ctrl_words_ = size_t(std::max(next_block, 1)) * kWords;
+        ctrl_.Alloc(ctrl_words_ * 4);
+        Check(hipMemset(ctrl_.get(), 0, ctrl_words_ * 4), "zero ctrl");
+        int32_t *ctrl = ctrl_.as<int32_t>();
+
+        for (size_t i = 0; i < launches_.size(); ++i) {
+            Launch &L = launches_[i];
+            const NodeSpec &n = *L.node;
+            const TaskSpec &t = *L.task;
+            const int64_t rt = n.rows / NodeTiles(n);
+            const int64_t in_off = t.has_geom ? t.in_row_off : t.tile * rt;
+            const int64_t in_rows = t.has_geom ? t.in_rows : rt;
+            if (L.publish) L.flag = flag_base.at(n.id) + t.tile;
+            if (sync_ == "event") {
+                if (L.publish) Check(hipEventCreateWithFlags(&L.pub_event, hipEventDisableTiming), "event");
+                continue;
+            }
+            // group waits by producer node
+            std::map<std::string, std::vector<int>> by_prod;
+            for (const auto &w : t.waits) by_prod[w.first].push_back(w.second);
+            for (auto &kv : by_prod) {
+                const NodeSpec &P = doc_.Node(kv.first);
+                std::sort(kv.second.begin(), kv.second.end());
+                const int ptiles = NodeTiles(P);
+                const int64_t prows = OutRows(P) / ptiles;
+                const int sbase = state_base.at({n.id, P.id});
+                std::vector<int> adv;
+                for (int k : kv.second)
+                    if (last_waiter.at(std::make_tuple(n.id, P.id, k)) == i) {
+                        adv.push_back(k);
+                        consumed_states_.push_back(sbase + k);
+                    }
+                // tiles intersecting this task's input rows in P's output row space
+                std::vector<int> hits;
+                for (int k = 0; k < ptiles; ++k)
+                    if (k * prows < in_off + in_rows && (k + 1) * prows > in_off) hits.push_back(k);
+                const bool contiguous_adv =
+                    adv.empty() || (adv.back() - adv.front() + 1 == int(adv.size()));
+                const bool fusable = wait_kind_ == "fused" && by_prod.size() == 1 && n.op != Op::MatMul &&
+                                     hits == kv.second && contiguous_adv;
+                if (fusable) {
+                    L.fused_wait = true;
+                    L.wait.ctrl = ctrl;
+                    L.wait.flag0 = flag_base.at(P.id);
+                    L.wait.state0 = sbase;
+                    L.wait.prod_rows = int(prows);
+                    L.wait.row_off = int(in_off);
+                    L.wait.adv_lo = adv.empty() ? 0 : adv.front();
+                    L.wait.adv_hi = adv.empty() ? 0 : adv.back() + 1;
+                    L.wait.max_spins = max_spins_;
+                    L.tile_rows = int(std::min<int64_t>(in_rows, prows));
+                } else {
+                    for (int k : kv.second) {
+                        RelayWait w{};
+                        w.ctrl = ctrl;
+                        w.flag0 = flag_base.at(P.id) + k;
+                        w.state0 = sbase + k;
+                        w.prod_rows = 1;
+                        w.row_off = 0;
+                        const bool advance = std::find(adv.begin(), adv.end(), k) != adv.end();
+                        w.adv_lo = 0;
+                        w.adv_hi = advance ? 1 : 0;
+                        w.max_spins = max_spins_;
+                        L.extra_waits.push_back(w);
+                    }
+                }
+            }
+        }
+        if (sync_ == "event") {
+            for (auto &L : launches_)
+                for (const auto &w : L.task->waits) L.wait_events.push_back(launches_[launch_of.at(w)].pub_event);
+        }
+        // enqueue order: global topological order (records before waits)
+        auto order = TopoOrder(doc_);
+        for (const auto &o : order) {
+            const auto &t = doc_.lanes[o.first].tasks[o.second];
+            enqueue_order_.push_back(launch_of.at({t.node, t.tile}));
+        }
+    }
+
+    hipStream_t StreamOf(int lane) const { return lane == 0 ? streams_.prod : streams_.cons; }
+
+    void EnqueueTask(RankCtx &rc, Launch &L, hipStream_t s)
+    {
+        const NodeSpec &n = *L.node;
+        const TaskSpec &t = *L.task;
+        NodeBuf &b = rc.bufs.at(n.id);
+        const int64_t rt = n.rows / NodeTiles(n);
+        const int64_t in_off = t.has_geom ? t.in_row_off : t.tile * rt;
+        const int64_t in_rows = t.has_geom ? t.in_rows : rt;
+        const int64_t out_off = t.has_geom ? t.out_row_off : t.tile * rt;
+        const void *in_base = n.preds.empty() ? b.own_in.get() : rc.bufs.at(n.preds[0]).out.get();
+        const size_t in_elem = 2;
+        const auto *in_tile = static_cast<const char *>(in_base) + size_t(in_off) * InCols(n) * in_elem;
+        const void *x1 = nullptr;
+        if (IsBinary(n.op)) {
+            const void *x1base = n.preds.size() > 1 ? rc.bufs.at(n.preds[1]).out.get() : b.aux.get();
+            x1 = static_cast<const char *>(x1base) + size_t(in_off) * n.cols * 2;
+        }
+        char *out_tile = static_cast<char *>(b.out.get()) + size_t(out_off) * n.cols * DTypeBytes(n.out_dtype);
+
+        if (sync_ == "event") {
+            for (hipEvent_t e : L.wait_events) Check(hipStreamWaitEvent(s, e, 0), "stream wait event");
+        }
+        for (const auto &w : L.extra_waits) WaitLaunch(w, 0, 1, s);
+
+        RelayPub pub{};
+        if (L.publish && sync_ == "flag") {
+            pub.ctrl = ctrl_.as<int32_t>();
+            pub.flag0 = L.flag;
+            pub.rows_per_tile = int(in_rows);
+        }
+        const RelayWait wait = L.fused_wait ? L.wait : RelayWait{};
+        const int grid = L.fused_wait ? relay_grid_ : 0;
+
+        switch (n.op) {
+            case Op::MatMul: {
+                GemmDesc d;
+                d.dtype = n.dtype;
+                d.A = in_tile;
+                d.lda = n.k;
+                const int64_t ncols = t.n_tile > 0 ? t.n_tile : n.n;
+                d.Bt = b.bt.as<uint16_t>() + size_t(t.n_off) * n.k;
+                d.ldb = n.k;
+                d.C = reinterpret_cast<uint16_t *>(out_tile) + (t.n_tile > 0 ? t.n_off : 0);
+                d.ldc = n.n;
+                d.M = int(in_rows);
+                d.N = int(ncols);
+                d.K = int(n.k);
+                if (pub.ctrl && GemmPickTile(d.M, d.N, pub.rows_per_tile).bm < 0) {
+                    // the tile cannot be one GEMM relay tile: release after the GEMM
+                    GemmLaunch(d, s);
+                    PublishLaunch(pub, 0, s);
+                } else {
+                    d.pub = pub;
+                    GemmLaunch(d, s);
+                }
+                break;
+            }
+            case Op::Gelu:
+            case Op::Silu:
+            case Op::Cast:
+            case Op::Add:
+            case Op::Mul:
+            case Op::Swiglu: {
+                EwDesc d;
+                d.op = n.op == Op::Gelu ? kEwGelu
+                     : n.op == Op::Silu ? kEwSilu
+                     : n.op == Op::Cast ? kEwCast
+                     : n.op == Op::Add  ? kEwAdd
+                     : n.op == Op::Mul  ? kEwMul
+                                        : kEwSwiglu;
+                d.dtype_in = n.dtype;
+                d.dtype_out = n.out_dtype;
+                d.x0 = in_tile;
+                d.x1 = x1;
+                d.y = out_tile;
+                d.rows = int(in_rows);
+                d.cols = int(n.cols);
+                d.tile_rows = L.fused_wait ? L.tile_rows : 0;
+                d.grid = grid;
+                d.wait = wait;
+                d.pub = pub;
+                if (pub.ctrl && d.tile_rows > 0 && d.tile_rows != d.rows) {
+                    // publish once for the whole task: release after the kernel
+                    d.pub = RelayPub{};
+                    EwLaunch(d, s);
+                    PublishLaunch(pub, 0, s);
+                } else {
+                    EwLaunch(d, s);
+                }
+                break;
+            }
+            case Op::Softmax:
+            case Op::RmsNorm:
+            case Op::AddRmsNorm: {
+                RowDesc d;
+                d.op = n.op == Op::Softmax ? kRowSoftmax : (n.op == Op::RmsNorm ? kRowRmsNorm : kRowAddRmsNorm);
+                d.dtype = n.dtype;
+                d.x0 = in_tile;
+                d.x1 = x1;
+                d.gamma = b.gamma.get();
+                d.y = out_tile;
+                d.sum_out = b.sum.get() ? static_cast<char *>(b.sum.get()) + size_t(out_off) * n.cols * 2 : nullptr;
+                d.rows = int(in_rows);
+                d.cols = int(n.cols);
+                d.eps = n.eps;
+                d.tile_rows = L.fused_wait ? L.tile_rows : 0;
+                d.grid = grid;
+                d.wait = wait;
+                d.pub = pub;
+                if (pub.ctrl && d.tile_rows > 0 && d.tile_rows != d.rows) {
+                    d.pub = RelayPub{};
+                    RowLaunch(d, s);
+                    PublishLaunch(pub, 0, s);
+                } else {
+                    RowLaunch(d, s);
+                }
+                break;
+            }
+        }
+        Check(hipGetLastError(), "task launch");
+        if (L.publish && sync_ == "event") Check(hipEventRecord(L.pub_event, s), "record event");
+    }
+
+    void EnqueueRank(int r)
+    {
+        for (size_t idx : enqueue_order_) {
+            Launch &L = launches_[idx];
+            EnqueueTask(ranks_[r], L, StreamOf(L.lane));
+        }
+    }
+
+    void Capture()
+    {
+        for (int r = 0; r < doc_.nranks; ++r) {
+            if (sync_ == "event") {
+                // one multi-stream graph: fork the consumer stream off the producer
+                hipGraph_t g = nullptr;
+                Check(hipStreamBeginCapture(streams_.prod, hipStreamCaptureModeThreadLocal), "begin capture");
+                hipEvent_t fork = nullptr, join = nullptr;
+                Check(hipEventCreateWithFlags(&fork, hipEventDisableTiming), "fork event");
+                Check(hipEventCreateWithFlags(&join, hipEventDisableTiming), "join event");
+                Check(hipEventRecord(fork, streams_.prod), "fork");
+                Check(hipStreamWaitEvent(streams_.cons, fork, 0), "fork wait");
+                EnqueueRank(r);
+                Check(hipEventRecord(join, streams_.cons), "join");
+                Check(hipStreamWaitEvent(streams_.prod, join, 0), "join wait");
+                Check(hipStreamEndCapture(streams_.prod, &g), "end capture");
+                hipGraphExec_t ex = nullptr;
+                Check(hipGraphInstantiate(&ex, g, nullptr, nullptr, 0), "instantiate");
+                graphs_.push_back({g, ex, 0, r});
+                (void)hipEventDestroy(fork);
+                (void)hipEventDestroy(join);
+                continue;
+            }
+            // flags: one graph per stream, replayed on that stream
+            for (int lane = 0; lane < 2; ++lane) {
+                bool any = false;
+                for (size_t idx : enqueue_order_)
+                    if (launches_[idx].lane == lane) any = true;
+                if (!any) continue;
+                hipStream_t s = StreamOf(lane);
+                hipGraph_t g = nullptr;
+                Check(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal), "begin capture");
+                for (size_t idx : enqueue_order_) {
+                    Launch &L = launches_[idx];
+                    if (L.lane == lane) EnqueueTask(ranks_[r], L, s);
+                }
+                Check(hipStreamEndCapture(s, &g), "end capture");
+                hipGraphExec_t ex = nullptr;
+                Check(hipGraphInstantiate(&ex, g, nullptr, nullptr, 0), "instantiate");
+                graphs_.push_back({g, ex, lane, r});
+            }
+        }
+    }
+
+    struct Graph {
+        hipGraph_t graph;
+        hipGraphExec_t exec;
+        int lane;
+        int rank;
+    };
+
+    SchedDoc doc_;
+    int device_;
+    std::string mode_;
+    std::string sync_;
+    std::string wait_kind_;
+    int relay_grid_ = 64;
+    uint32_t max_spins_ = kDefaultMaxSpins;
+    StreamPair streams_;
+    hipEvent_t ev0_ = nullptr, ev1_ = nullptr, ev2_ = nullptr;
+    std::vector<RankCtx> ranks_;
+    std::vector<Launch> launches_;
+    std::vector<size_t> enqueue_order_;
+    std::vector<int> consumed_states_;
+    DevBuf ctrl_;
+    size_t ctrl_words_ = 0;
+    std::vector<Graph> graphs_;
+};
+
+int ParseDevice(const char *devices)
+{
+    if (devices == nullptr || *devices == '\0') return 0;
+    std::string s(devices);
+    int dev = -1;
+    std::stringstream ss(s);
+    std::string tok;
+    while (std::getline(ss, tok, ',')) {
+        if (tok.empty()) throw std::runtime_error("devices has an empty entry");
+        const int d = std::stoi(tok);
+        if (dev >= 0 && d != dev) throw std::runtime_error("all ranks must run on the one device of this target");
+        dev = d;
+    }
+    return dev < 0 ? 0 : dev;
+}
+
+int RunPlan(const char *schedule_json, int iters, int warmup, const char *devices, const char *mode,
+            const char *out_json)
+{
+    try {
+        if (iters < 1 || warmup < 0) {
+            std::fprintf(stderr, "kr_plan_run: iters must be >= 1 and warmup >= 0\n");
+            return 2;
+        }
+        const Value root = json::ParseFile(schedule_json);
+        SchedDoc doc = ParseSchedule(root);
+        NormalizeTopology(doc);
+        const int device = ParseDevice(devices);
+        Executor ex(std::move(doc), device, mode ? mode : "direct");
+        ex.Prepare();
+        for (int i = 0; i < warmup; ++i) (void)ex.RunOnce(nullptr);
+        std::vector<double> times, dev;
+        for (int i = 0; i < iters; ++i) {
+            double d = 0.0;
+            times.push_back(ex.RunOnce(&d));
+            dev.push_back(d);
+        }
+        const int timeouts = ex.FlagTimeouts();
+        const double checksum = ex.Checksum();
+        const std::string dump = EnvStr("KR_DUMP_DIR", "");
+        if (!dump.empty()) ex.Dump(dump);
+
+        Value result = Value::MakeObject();
+        result.Set("dag", Value::MakeString(ex.doc().dag));
+        result.Set("group", Value::MakeString(ex.doc().group));
+        result.Set("nranks", Value::MakeNumber(ex.doc().nranks));
+        result.Set("iters", Value::MakeNumber(iters));
+        result.Set("warmup", Value::MakeNumber(warmup));
+        result.Set("p50_us", Value::MakeNumber(Median(times)));
+        result.Set("gate_timeouts", Value::MakeNumber(timeouts));
+        result.Set("checksum", Value::MakeNumber(checksum));
+        result.Set("ok", Value::MakeBool(timeouts == 0));
+        Value arr = Value::MakeArray();
+        for (double t : times) arr.Push(Value::MakeNumber(t));
+        result.Set("times_us", arr);
+        result.Set("best_us", Value::MakeNumber(Min(times)));
+        Value darr = Value::MakeArray();
+        for (double t : dev) darr.Push(Value::MakeNumber(t));
+        result.Set("device_us", darr);
+        result.Set("device_best_us", Value::MakeNumber(Min(dev)));
+        result.Set("device_p50_us", Value::MakeNumber(Median(dev)));
+        result.Set("sync", Value::MakeString(ex.sync()));
+        result.Set("mode", Value::MakeString(mode ? mode : "direct"));
+        result.Set("flag_edges", Value::MakeNumber(ex.edges()));
+        result.Set("consumer_cus", Value::MakeNumber(ex.consumer_cus()));
+        json::WriteFile(out_json, result);
+        std::printf("%s\n", result.Dump().c_str());
+        std::fflush(stdout);
+        return 0;
+    } catch (const std::exception &e) {
+        std::fprintf(stderr, "kr_plan_run error: %s\n", e.what());
+        std::fflush(stderr);
+        return 1;
+    }
+}
+
+}  // namespace plan
+}  // namespace kr
+
+extern "C" int kr_plan_run(const char *schedule_json, int iters, int warmup, const char *devices, const char *mode,
+                           const char *out_json)
+{
+    if (schedule_json == nullptr || out_json == nullptr) return 2;
+    return kr::plan::RunPlan(schedule_json, iters, warmup, devices, mode, out_json);
+}

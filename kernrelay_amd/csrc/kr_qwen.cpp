@@ -1,0 +1,1104 @@
+// Single-GPU Qwen2.5 / Qwen3-text prefill runtime behind kr_qwen_run and
+// kr_qwen_profile_many: the MI355X counterpart of the reference's class Qwen
+// (exec/qwen_main.cpp:211-1803).
+//
+// Model directory = the reference's export format (scripts/export_model.py:
+// 142-226): manifest.json, weights.bin (bf16, matmul weights as weight_t
+// [K,N]), ids.bin (int64 [seq]), optional ref_last_logits.bin / ref.json.
+//
+// HBM layout (built once at load):
+//   * every matmul weight is transposed to Bt [N,K] (K contiguous, the MFMA
+//     operand layout);
+//   * q/k/v weights (and biases) are concatenated into one [(HQ+2HKV)*D, H]
+//     projection, so QKV is one GEMM whose bias add is fused in its epilogue;
+//   * gate/up are concatenated into one [2I, H] projection, interleaved in
+//     groups of 8 rows (8 gate, 8 up, ...), so one GEMM writes a [S, 2I] tile
+//     the SwiGLU consumer reads as contiguous 16-element chunks;
+//   * all weights share one allocation (the reference keeps one block too,
+//     exec/qwen_main.cpp:408-428).
+// Per-element arithmetic is identical to separate q/k/v/gate/up matmuls:
+// every GEMM row uses the same MFMA sequence and K order.
+//
+// Op order follows BuildSerial (exec/qwen_main.cpp:925-992) and EmitQkNorm
+// (:1346-1357). Modes:
+//   serial / serial_graph      one stream, Add and RmsNorm as separate kernels
+//   serial_fused / graph_whole one stream, fused Add+RMSNorm
+//   relay_event                two streams, whole ops, hipEvent edges
+//   relay_flag(_graph)         two streams, whole ops, device-flag edges
+//   relay_split[:k]            two streams, device flags, the o, gate/up and
+//                              down producers release k row tiles from their
+//                              epilogues and the Add+RMSNorm / SwiGLU
+//                              consumers start per tile (per-stream graphs)
+// The producer stream runs GEMMs, RoPE and attention; the consumer stream runs
+// Add+RMSNorm and SwiGLU (the reference's AIC/AIV split, BuildDual :811-923).
+#include <fcntl.h>
+#include <sys/mman.h>
+#include <sys/stat.h>
+#include <unistd.h>
+
+#include <cmath>
+#include <cstdio>
+#include <fstream>
+#include <functional>
+#include <map>
+#include <sstream>
+
+#include "../../include/kernrelay.h"
+#include "kr_gemm.h"
+#include "kr_json.h"
+#include "kr_misc.h"
+#include "kr_rowops.h"
+#include "kr_runtime.h"
+
+namespace kr {
+namespace qwen {
+
+using json::Value;
+
+struct Mode {
+    std::string name;
+    bool dual = false;     // producer + consumer streams
+    bool flags = false;    // device flags (else events) between the streams
+    bool graph = false;    // capture and replay
+    bool fused = false;    // fused Add+RMSNorm
+    int tiles = 1;         // relay row tiles
+    bool split = false;    // tile-released consumers with in-kernel waits
+};
+
+Mode ParseMode(const std::string &m)
+{
+    Mode md;
+    md.name = m;
+    if (m == "serial") {
+    } else if (m == "serial_fused") {
+        md.fused = true;
+    } else if (m == "serial_graph") {
+        md.graph = true;
+    } else if (m == "graph_whole") {
+        md.graph = md.fused = true;
+    } else if (m == "relay_event") {
+        md.dual = md.fused = true;
+    } else if (m == "relay_flag") {
+        md.dual = md.flags = md.fused = true;
+    } else if (m == "relay_flag_graph") {
+        md.dual = md.flags = md.fused = md.graph = true;
+    } else if (m.rfind("relay_split", 0) == 0) {
+        md.dual = md.flags = md.fused = md.graph = md.split = true;
+        md.tiles = 4;
+        if (m.size() > 11) {
+            if (m[11] != ':') throw std::runtime_error("unknown mode " + m);
+            md.tiles = std::atoi(m.c_str() + 12);
+        } else if (const char *e = std::getenv("KR_RELAY_TILES")) {
+            md.tiles = std::atoi(e);
+        }
+        if (md.tiles < 1 || md.tiles > 8) throw std::runtime_error("relay_split tiles must be in 1..8");
+    } else if (m.rfind("pp", 0) == 0 || m.rfind("tp", 0) == 0) {
+        throw std::runtime_error("multi-GPU not in scope");
+    } else {
+        throw std::runtime_error("unknown mode " + m);
+    }
+    return md;
+}
+
+struct Item {
+    int stream;  // 0 = producer, 1 = consumer
+    std::function<void(hipStream_t)> fn;
+};
+
+struct TensorInfo {
+    size_t offset = 0, bytes = 0;
+    std::vector<int64_t> shape;
+};
+
+class Model {
+public:
+    Model(std::string dir, int seq, int device, std::string mode)
+        : dir_(std::move(dir)), seq_(seq), device_(device), mode_(ParseMode(mode))
+    {
+    }
+
+    ~Model()
+    {
+        for (auto &g : graphs_) {
+            if (g.second) (void)hipGraphExecDestroy(g.second);
+            if (g.first) (void)hipGraphDestroy(g.first);
+        }
+        for (hipEvent_t e : events_) (void)hipEventDestroy(e);
+        if (t0_) (void)hipEventDestroy(t0_);
+        if (tp_) (void)hipEventDestroy(tp_);
+        if (tc_) (void)hipEventDestroy(tc_);
+        streams_.Destroy();
+        if (map_ && map_ != MAP_FAILED) munmap(map_, map_bytes_);
+        if (fd_ >= 0) close(fd_);
+    }
+
+    void Build(bool program = true)
+    {
+        const auto t0 = Clock::now();
+        Check(hipSetDevice(device_), "hipSetDevice");
+        streams_.Create(device_);
+        Check(hipEventCreate(&t0_), "event");
+        Check(hipEventCreate(&tp_), "event");
+        Check(hipEventCreate(&tc_), "event");
+        LoadManifest();
+        LoadWeights();
+        UploadIds();
+        Allocate();
+        load_ms_ = Us(t0, Clock::now()) / 1000.0;
+        if (program) {
+            BuildProgram();
+            if (mode_.graph) Capture();
+        }
+    }
+
+    void RunOnce()
+    {
+        if (!graphs_.empty()) {
+            for (size_t s = 0; s < graphs_.size(); ++s)
+                if (graphs_[s].second) Check(hipGraphLaunch(graphs_[s].second, Stream(int(s))), "graph launch");
+            return;
+        }
+        for (auto &it : prog_) it.fn(Stream(it.stream));
+    }
+
+    void Bench(int warmup, int iters)
+    {
+        for (int i = 0; i < warmup; ++i) {
+            RunOnce();
+            Check(hipDeviceSynchronize(), "warmup sync");
+        }
+        samples_.clear();
+        host_samples_.clear();
+        dev_samples_.clear();
+        for (int i = 0; i < iters; ++i) {
+            Check(hipDeviceSynchronize(), "pre sync");
+            const auto t0 = Clock::now();
+            Check(hipEventRecord(t0_, streams_.prod), "record t0");
+            Check(hipStreamWaitEvent(streams_.cons, t0_, 0), "cons start");
+            RunOnce();
+            const auto th = Clock::now();
+            Check(hipEventRecord(tp_, streams_.prod), "record tp");
+            Check(hipEventRecord(tc_, streams_.cons), "record tc");
+            Check(hipDeviceSynchronize(), "post sync");
+            const auto t1 = Clock::now();
+            float a = 0.f, b = 0.f;
+            Check(hipEventElapsedTime(&a, t0_, tp_), "elapsed");
+            Check(hipEventElapsedTime(&b, t0_, tc_), "elapsed");
+            samples_.push_back(Us(t0, t1));
+            host_samples_.push_back(Us(t0, th));
+            dev_samples_.push_back(1000.0 * std::max(a, b));
+        }
+    }
+
+    void Verify()
+    {
+        const size_t V = size_t(V_);
+        std::vector<uint16_t> last(V);
+        const uint16_t *lp = logits_.as<uint16_t>() + size_t(seq_ - 1) * V;
+        Check(hipMemcpy(last.data(), lp, V * 2, hipMemcpyDeviceToHost), "logits d2h");
+        std::vector<float> ref;
+        {
+            std::ifstream rf(dir_ + "/ref_last_logits.bin", std::ios::binary | std::ios::ate);
+            if (rf && size_t(rf.tellg()) == V * 4) {
+                ref.resize(V);
+                rf.seekg(0);
+                rf.read(reinterpret_cast<char *>(ref.data()), std::streamsize(V * 4));
+            }
+        }
+        double mx = 0.0, sum = 0.0;
+        float best = -INFINITY, second = -INFINITY;
+        int arg = 0;
+        for (size_t i = 0; i < V; ++i) {
+            const float v = HostBF16ToF32(last[i]);
+            if (!ref.empty()) mx = std::max(mx, std::fabs(double(v) - double(ref[i])));
+            sum += std::fabs(double(v));
+            if (v > best) {
+                second = best;
+                best = v;
+                arg = int(i);
+            } else if (v > second) {
+                second = v;
+            }
+        }
+        argmax_ = arg;
+        margin_ = double(best) - double(second);
+        maxdiff_ = ref.empty() ? -1.0 : mx;
+        absmean_ = sum / double(V);
+        ref_argmax_ = -1;
+        std::ifstream jf(dir_ + "/ref.json");
+        if (jf) ref_argmax_ = int(json::ParseFile(dir_ + "/ref.json").Num("argmax_last", -1));
+        // FNV-1a over every logit: the bit-exactness witness across modes.
+        std::vector<uint16_t> all(size_t(seq_) * V);
+        Check(hipMemcpy(all.data(), logits_.get(), all.size() * 2, hipMemcpyDeviceToHost), "logits d2h");
+        uint64_t h = 1469598103934665603ull;
+        const auto *bytes = reinterpret_cast<const uint8_t *>(all.data());
+        for (size_t i = 0; i < all.size() * 2; ++i) h = (h ^ bytes[i]) * 1099511628211ull;
+        fnv_ = h;
+        flag_edges_ = int(consumed_.size());
+        flag_timeouts_ = 0;
+        if (!consumed_.empty()) {
+            std::vector<int32_t> host(ctrl_blocks_ * kWords);
+            Check(hipMemcpy(host.data(), ctrl_.get(), host.size() * 4, hipMemcpyDeviceToHost), "ctrl d2h");
+            for (int s : consumed_)
+                if (host[size_t(s) * kWords + kOffStatus] != 1) ++flag_timeouts_;
+        }
+        const std::string dump = EnvStr("KR_DUMP_DIR", "");
+        if (!dump.empty()) {
+            std::ofstream f(dump + "/last_logits_bf16.bin", std::ios::binary);
+            f.write(reinterpret_cast<const char *>(last.data()), std::streamsize(V * 2));
+        }
+    }
+
+    std::string ResultJson(int warmup, int iters) const
+    {
+        Value r = Value::MakeObject();
+        r.Set("mode", Value::MakeString(mode_.name));
+        r.Set("seq", Value::MakeNumber(seq_));
+        r.Set("device", Value::MakeNumber(device_));
+        r.Set("warmup", Value::MakeNumber(warmup));
+        r.Set("iters", Value::MakeNumber(iters));
+        r.Set("best_us", Value::MakeNumber(Min(samples_)));
+        r.Set("typical_us", Value::MakeNumber(Median(samples_)));
+        Value arr = Value::MakeArray();
+        for (double s : samples_) arr.Push(Value::MakeNumber(s));
+        r.Set("samples_us", arr);
+        r.Set("argmax", Value::MakeNumber(argmax_));
+        r.Set("ref_argmax", Value::MakeNumber(ref_argmax_));
+        r.Set("maxdiff", maxdiff_ < 0 ? Value() : Value::MakeNumber(maxdiff_));
+        r.Set("abs_mean", Value::MakeNumber(absmean_));
+        r.Set("flag_edges", Value::MakeNumber(flag_edges_));
+        r.Set("flag_timeouts", Value::MakeNumber(flag_timeouts_));
+        r.Set("host_best_us", Value::MakeNumber(Min(host_samples_)));
+        r.Set("host_typical_us", Value::MakeNumber(Median(host_samples_)));
+        // additions of this build
+        r.Set("tiles", Value::MakeNumber(mode_.tiles));
+        r.Set("device_best_us", Value::MakeNumber(Min(dev_samples_)));
+        r.Set("device_typical_us", Value::MakeNumber(Median(dev_samples_)));
+        const double best = Min(samples_);
+        r.Set("tok_s", Value::MakeNumber(best > 0 ? seq_ * 1e6 / best : 0.0));
+        char buf[32];
+        std::snprintf(buf, sizeof buf, "%016llx", static_cast<unsigned long long>(fnv_));
+        r.Set("logits_fnv64", Value::MakeString(buf));
+        r.Set("last_top2_margin", Value::MakeNumber(margin_));
+        r.Set("consumer_cus", Value::MakeNumber(streams_.cons_cus));
+        r.Set("load_ms", Value::MakeNumber(load_ms_));
+        r.Set("kernels_per_run", Value::MakeNumber(double(prog_.size())));
+        return r.Dump();
+    }
+
+    std::string ProfileMany(const std::string &spec_path);
+
+private:
+    hipStream_t Stream(int s) const { return s == 0 ? streams_.prod : streams_.cons; }
+
+    std::string LP(int l) const
+    {
+        char b[8];
+        std::snprintf(b, sizeof b, "L%02d.", l);
+        return b;
+    }
+
+    // ------------------------------------------------------------ loading
+    void LoadManifest()
+    {
+        const Value doc = json::ParseFile(dir_ + "/manifest.json");
+        const Value &cfg = doc.At("config");
+        H_ = int(cfg.At("hidden_size").AsNumber());
+        I_ = int(cfg.At("intermediate_size").AsNumber());
+        L_ = int(cfg.At("num_hidden_layers").AsNumber());
+        HQ_ = int(cfg.At("num_attention_heads").AsNumber());
+        HKV_ = int(cfg.At("num_key_value_heads").AsNumber());
+        V_ = int(cfg.At("vocab_size").AsNumber());
+        D_ = cfg.Has("head_dim") ? int(cfg.At("head_dim").AsNumber()) : H_ / HQ_;
+        qk_norm_ = cfg.Flag("qk_norm", false);
+        eps_ = cfg.Num("rms_norm_eps", 1e-6);
+        for (const auto &kv : doc.At("tensors").Members()) {
+            TensorInfo t;
+            t.offset = size_t(kv.second.At("offset").AsNumber());
+            t.bytes = size_t(kv.second.At("bytes").AsNumber());
+            for (const auto &d : kv.second.At("shape").Items()) t.shape.push_back(int64_t(d.AsNumber()));
+            tensors_[kv.first] = t;
+        }
+        const bool attn_bias = cfg.Flag("attention_bias", true);
+        qkv_bias_ = attn_bias && tensors_.count("L00.q_proj.bias") != 0;
+        max_pos_ = int(doc.Num("max_pos", 4096));
+        if (int(doc.Num("seq", seq_)) != seq_) throw std::runtime_error("manifest seq mismatch");
+        if (seq_ <= 0 || seq_ > max_pos_) throw std::runtime_error("seq must be in 1..max_pos");
+        if (HQ_ % HKV_ != 0) throw std::runtime_error("num_attention_heads must be a multiple of num_key_value_heads");
+        if (D_ != 64 && D_ != 128) throw std::runtime_error("head_dim must be 64 or 128");
+        if (H_ % 8 != 0 || I_ % 8 != 0) throw std::runtime_error("hidden/intermediate sizes must be multiples of 8");
+    }
+
+    const TensorInfo &T(const std::string &name, std::vector<int64_t> shape) const
+    {
+        auto it = tensors_.find(name);
+        if (it == tensors_.end()) throw std::runtime_error("weights: missing tensor " + name);
+        const TensorInfo &t = it->second;
+        int64_t n = 1;
+        for (auto d : shape) n *= d;
+        int64_t m = 1;
+        for (auto d : t.shape) m *= d;
+        if (n != m || t.bytes != size_t(n) * 2)
+            throw std::runtime_error("weights: tensor " + name + " has unexpected shape/bytes");
+        if (t.offset + t.bytes > map_bytes_) throw std::runtime_error("weights: tensor " + name + " beyond weights.bin");
+        return t;
+    }
+
+    const void *Host(const TensorInfo &t) const { return static_cast<const char *>(map_) + t.offset; }
+
+    size_t Carve(size_t bytes)
+    {
+        const size_t off = wcursor_;
+        wcursor_ += (bytes + 255) & ~size_t(255);
+        return off;
+    }
+
+    void LoadWeights()
+    {
+        fd_ = open((dir_ + "/weights.bin").c_str(), O_RDONLY);
+        if (fd_ < 0) throw std::runtime_error("open weights.bin");
+        struct stat st {};
+        fstat(fd_, &st);
+        map_bytes_ = size_t(st.st_size);
+        map_ = mmap(nullptr, map_bytes_, PROT_READ, MAP_PRIVATE, fd_, 0);
+        if (map_ == MAP_FAILED) throw std::runtime_error("mmap weights.bin");
+
+        const int NQKV = (HQ_ + 2 * HKV_) * D_;
+        ldqkv_ = NQKV;
+        // sub-allocation plan
+        struct LayerOff { size_t qkv, bias, o, gu, down, ln1, ln2, qn, kn; };
+        std::vector<LayerOff> lo(L_);
+        for (int l = 0; l < L_; ++l) {
+            lo[l].qkv = Carve(size_t(NQKV) * H_ * 2);
+            lo[l].bias = qkv_bias_ ? Carve(size_t(NQKV) * 2) : 0;
+            lo[l].o = Carve(size_t(H_) * HQ_ * D_ * 2);
+            lo[l].gu = Carve(size_t(2) * I_ * H_ * 2);
+            lo[l].down = Carve(size_t(H_) * I_ * 2);
+            lo[l].ln1 = Carve(size_t(H_) * 2);
+            lo[l].ln2 = Carve(size_t(H_) * 2);
+            lo[l].qn = qk_norm_ ? Carve(size_t(D_) * 2) : 0;
+            lo[l].kn = qk_norm_ ? Carve(size_t(D_) * 2) : 0;
+        }
+        const size_t off_embed = Carve(size_t(V_) * H_ * 2);
+        const size_t off_lm = Carve(size_t(V_) * H_ * 2);
+        const size_t off_fn = Carve(size_t(H_) * 2);
+        const size_t off_cos = Carve(size_t(seq_) * D_ * 2);
+        const size_t off_sin = Carve(size_t(seq_) * D_ * 2);
+        wbuf_.Alloc(wcursor_);
+        char *base = wbuf_.as<char>();
+        size_t max_mat = std::max({size_t(V_) * H_, size_t(I_) * H_, size_t(NQKV) * H_, size_t(HQ_) * D_ * H_}) * 2;
+        DevBuf stage(max_mat), stage2(size_t(I_) * H_ * 2);
+        hipStream_t s = streams_.prod;
+
+        auto put_plain = [&](const TensorInfo &t, size_t dst) {
+            Check(hipMemcpy(base + dst, Host(t), t.bytes, hipMemcpyHostToDevice), "weights h2d");
+        };
+        // weight_t [K,N] -> Bt rows [row0, row0+N) of a [*, K] matrix
+        auto put_bt = [&](const TensorInfo &t, int K, int N, char *dst_rows) {
+            Check(hipMemcpy(stage.get(), Host(t), t.bytes, hipMemcpyHostToDevice), "weights h2d");
+            TransposeLaunch(stage.get(), dst_rows, K, N, s);
+            Check(hipStreamSynchronize(s), "transpose sync");
+        };
+        for (int l = 0; l < L_; ++l) {
+            const std::string p = LP(l);
+            char *qkv = base + lo[l].qkv;
+            put_bt(T(p + "q_proj.weight_t", {H_, HQ_ * D_}), H_, HQ_ * D_, qkv);
+            put_bt(T(p + "k_proj.weight_t", {H_, HKV_ * D_}), H_, HKV_ * D_, qkv + size_t(HQ_) * D_ * H_ * 2);
+            put_bt(T(p + "v_proj.weight_t", {H_, HKV_ * D_}), H_, HKV_ * D_,
+                   qkv + size_t(HQ_ + HKV_) * D_ * H_ * 2);
+            if (qkv_bias_) {
+                char *b = base + lo[l].bias;
+                put_plain(T(p + "q_proj.bias", {HQ_ * D_}), lo[l].bias);
+                Check(hipMemcpy(b + size_t(HQ_) * D_ * 2, Host(T(p + "k_proj.bias", {HKV_ * D_})),
+                                size_t(HKV_) * D_ * 2, hipMemcpyHostToDevice), "bias h2d");
+                Check(hipMemcpy(b + size_t(HQ_ + HKV_) * D_ * 2, Host(T(p + "v_proj.bias", {HKV_ * D_})),
+                                size_t(HKV_) * D_ * 2, hipMemcpyHostToDevice), "bias h2d");
+            }
+            put_bt(T(p + "o_proj.weight_t", {HQ_ * D_, H_}), HQ_ * D_, H_, base + lo[l].o);
+            // gate/up: transpose each into [I, H], then interleave 8-row groups
+            for (int which = 0; which < 2; ++which) {
+                const TensorInfo &t = T(p + (which ? "up_proj.weight_t" : "gate_proj.weight_t"), {H_, I_});
+                Check(hipMemcpy(stage.get(), Host(t), t.bytes, hipMemcpyHostToDevice), "weights h2d");
+                TransposeLaunch(stage.get(), stage2.get(), H_, I_, s);
+                Check(hipStreamSynchronize(s), "transpose sync");
+                const size_t grp = size_t(8) * H_ * 2;
+                Check(hipMemcpy2D(base + lo[l].gu + which * grp, 2 * grp, stage2.get(), grp, grp, size_t(I_ / 8),
+                                  hipMemcpyDeviceToDevice), "interleave gate/up");
+            }
+            put_bt(T(p + "down_proj.weight_t", {I_, H_}), I_, H_, base + lo[l].down);
+            put_plain(T(p + "input_layernorm.weight", {H_}), lo[l].ln1);
+            put_plain(T(p + "post_attention_layernorm.weight", {H_}), lo[l].ln2);
+            if (qk_norm_) {
+                put_plain(T(p + "q_norm.weight", {D_}), lo[l].qn);
+                put_plain(T(p + "k_norm.weight", {D_}), lo[l].kn);
+            }
+            Layer ly;
+            ly.qkv = reinterpret_cast<uint16_t *>(qkv);
+            ly.bias = qkv_bias_ ? reinterpret_cast<uint16_t *>(base + lo[l].bias) : nullptr;
+            ly.o = reinterpret_cast<uint16_t *>(base + lo[l].o);
+            ly.gu = reinterpret_cast<uint16_t *>(base + lo[l].gu);
+            ly.down = reinterpret_cast<uint16_t *>(base + lo[l].down);
+            ly.ln1 = reinterpret_cast<uint16_t *>(base + lo[l].ln1);
+            ly.ln2 = reinterpret_cast<uint16_t *>(base + lo[l].ln2);
+            ly.qn = qk_norm_ ? reinterpret_cast<uint16_t *>(base + lo[l].qn) : nullptr;
+            ly.kn = qk_norm_ ? reinterpret_cast<uint16_t *>(base + lo[l].kn) : nullptr;
+            layers_.push_back(ly);
+        }
+        put_plain(T("embed.weight", {V_, H_}), off_embed);
+        put_bt(T("lm_head.weight_t", {H_, V_}), H_, V_, base + off_lm);
+        put_plain(T("final_norm.weight", {H_}), off_fn);
+        // rope tables [1,1,max_pos,D]: positions 0..seq-1
+        const TensorInfo &tc = T("rope.cos", {int64_t(max_pos_) * D_});
+        const TensorInfo &ts = T("rope.sin", {int64_t(max_pos_) * D_});
+        Check(hipMemcpy(base + off_cos, Host(tc), size_t(seq_) * D_ * 2, hipMemcpyHostToDevice), "rope h2d");
+        Check(hipMemcpy(base + off_sin, Host(ts), size_t(seq_) * D_ * 2, hipMemcpyHostToDevice), "rope h2d");
+        embed_ = reinterpret_cast<uint16_t *>(base + off_embed);
+        lm_ = reinterpret_cast<uint16_t *>(base + off_lm);
+        final_norm_ = reinterpret_cast<uint16_t *>(base + off_fn);
+        cos_ = reinterpret_cast<uint16_t *>(base + off_cos);
+        sin_ = reinterpret_cast<uint16_t *>(base + off_sin);
+        Check(hipDeviceSynchronize(), "weights sync");
+    }
+
+    void UploadIds()
+    {
+        std::ifstream f(dir_ + "/ids.bin", std::ios::binary | std::ios::ate);
+        if (!f) throw std::runtime_error("ids.bin");
+        const size_t bytes = size_t(f.tellg());
+        if (bytes != size_t(seq_) * 8) throw std::runtime_error("ids size != seq");
+        std::vector<int64_t> ids(seq_);
+        f.seekg(0);
+        f.read(reinterpret_cast<char *>(ids.data()), std::streamsize(bytes));
+        for (int64_t id : ids)
+            if (id < 0 || id >= V_) throw std::runtime_error("ids.bin holds a token id outside [0, vocab)");
+        ids_.Alloc(bytes);
+        Check(hipMemcpy(ids_.get(), ids.data(), bytes, hipMemcpyHostToDevice), "ids h2d");
+    }
+
+    void Allocate()
+    {
+        const size_t S = size_t(seq_);
+        auto a16 = [&](DevBuf &b, size_t elems) { b.Alloc(elems * 2); };
+        a16(h_[0], S * H_);
+        a16(h_[1], S * H_);
+        a16(x_, S * H_);
+        a16(qkv_, S * ldqkv_);
+        if (qk_norm_) {
+            a16(qn_, S * HQ_ * D_);
+            a16(kn_, S * HKV_ * D_);
+        }
+        a16(attn_, S * HQ_ * D_);
+        a16(o_, S * H_);
+        a16(gu_, S * 2 * I_);
+        a16(act_, S * I_);
+        a16(down_, S * H_);
+        a16(hf_, S * H_);
+        a16(xf_, S * H_);
+        a16(logits_, S * size_t(V_));
+        rstd_.Alloc(S * 4);
+    }
+
+    // ------------------------------------------------------------ program
+    void Emit(int s, std::function<void(hipStream_t)> fn) { prog_.push_back({mode_.dual ? s : 0, std::move(fn)}); }
+
+    // An edge of `tiles` relay blocks (block t = producer tile t's flag and
+    // the single consumer's state for it).
+    int NewEdge(int tiles)
+    {
+        const int e = int(ctrl_blocks_);
+        ctrl_blocks_ += size_t(tiles);
+        if (!mode_.flags) {
+            hipEvent_t ev = nullptr;
+            Check(hipEventCreateWithFlags(&ev, hipEventDisableTiming), "event");
+            events_.push_back(ev);
+            edge_event_[e] = ev;
+        }
+        return e;
+    }
+
+    RelayPub Pub(int edge, int rows_per_tile) const
+    {
+        RelayPub p{};
+        if (!mode_.flags) return p;
+        p.ctrl = ctrl_.as<int32_t>();
+        p.flag0 = edge;
+        p.rows_per_tile = rows_per_tile;
+        return p;
+    }
+
+    RelayWait WaitDesc(int edge, int tiles) const
+    {
+        RelayWait w{};
+        w.ctrl = ctrl_.as<int32_t>();
+        w.flag0 = edge;
+        w.state0 = edge;
+        w.prod_rows = seq_ / tiles;
+        w.row_off = 0;
+        w.adv_lo = 0;
+        w.adv_hi = tiles;
+        w.max_spins = max_spins_;
+        return w;
+    }
+
+    // Producer-side release for ops without a fused epilogue.
+    void PublishAfter(int s, int edge)
+    {
+        if (!mode_.dual) return;
+        if (mode_.flags) {
+            RelayPub p = Pub(edge, seq_);
+            Emit(s, [p](hipStream_t st) { PublishLaunch(p, 0, st); });
+        } else {
+            hipEvent_t ev = edge_event_.at(edge);
+            Emit(s, [ev](hipStream_t st) { Check(hipEventRecord(ev, st), "record edge"); });
+        }
+    }
+
+    // Whole-edge wait ahead of the next op on stream s.
+    void WaitBefore(int s, int edge, int tiles)
+    {
+        if (!mode_.dual) return;
+        if (mode_.flags) {
+            RelayWait w = WaitDesc(edge, tiles);
+            for (int t = 0; t < tiles; ++t) consumed_.push_back(edge + t);
+            const int S = seq_;
+            Emit(s, [w, S](hipStream_t st) { WaitLaunch(w, 0, S, st); });
+        } else {
+            hipEvent_t ev = edge_event_.at(edge);
+            Emit(s, [ev](hipStream_t st) { Check(hipStreamWaitEvent(st, ev, 0), "wait edge"); });
+        }
+    }
+
+    void Gemm(int s, const void *A, int64_t lda, const uint16_t *Bt, int N, int K, void *C, int64_t ldc,
+              const uint16_t *bias, int M, RelayPub pub)
+    {
+        GemmDesc d;
+        d.dtype = kBF16;
+        d.A = A;
+        d.lda = lda;
+        d.Bt = Bt;
+        d.ldb = K;
+        d.C = C;
+        d.ldc = ldc;
+        d.bias = bias;
+        d.M = M;
+        d.N = N;
+        d.K = K;
+        d.pub = pub;
+        Emit(s, [d](hipStream_t st) { GemmLaunch(d, st); });
+    }
+
+    void AddRmsNorm(int s, const void *a, const void *b, const uint16_t *g, void *y, void *sum, RelayWait w,
+                    int tile_rows, RelayPub pub, int grid)
+    {
+        if (mode_.fused) {
+            RowDesc d;
+            d.op = kRowAddRmsNorm;
+            d.x0 = a;
+            d.x1 = b;
+            d.gamma = g;
+            d.y = y;
+            d.sum_out = sum;
+            d.rstd_out = rstd_.as<float>();
+            d.rows = seq_;
+            d.cols = H_;
+            d.eps = float(eps_);
+            d.tile_rows = tile_rows;
+            d.grid = grid;
+            d.wait = w;
+            d.pub = pub;
+            Emit(s, [d](hipStream_t st) { RowLaunch(d, st); });
+            return;
+        }
+        EwDesc e;
+        e.op = kEwAdd;
+        e.x0 = a;
+        e.x1 = b;
+        e.y = sum;
+        e.rows = seq_;
+        e.cols = H_;
+        Emit(s, [e](hipStream_t st) { EwLaunch(e, st); });
+        RmsNorm(s, sum, g, y, seq_, H_, 1, 0);
+    }
+
+    void RmsNorm(int s, const void *x, const uint16_t *g, void *y, int rows, int cols, int group, int64_t ld)
+    {
+        RowDesc d;
+        d.op = kRowRmsNorm;
+        d.x0 = x;
+        d.gamma = g;
+        d.y = y;
+        d.rstd_out = rows == seq_ ? rstd_.as<float>() : nullptr;
+        d.rows = rows;
+        d.cols = cols;
+        d.in_group = group;
+        d.in_ld = ld;
+        d.eps = float(eps_);
+        Emit(s, [d](hipStream_t st) { RowLaunch(d, st); });
+    }
+
+    void BuildProgram()
+    {
+        const int S = seq_;
+        const int k = mode_.split ? mode_.tiles : 1;
+        if (mode_.split && (S % k != 0 || (S / k) % 64 != 0))
+            throw std::runtime_error("relay_split: seq/tiles must be a multiple of 64");
+        relay_grid_ = EnvInt("KR_RELAY_GRID", 64);
+        max_spins_ = uint32_t(EnvInt("KR_MAX_SPINS", int(kDefaultMaxSpins)));
+        const int P = 0, C = 1;
+        // Six edges per layer, each of k relay blocks (block t = producer tile
+        // t's flag and the single consumer's state for it).
+        struct LayerEdges { int o_ln2, ln2_gu, gu_act, act_down, down_ln, exit; };
+        std::vector<LayerEdges> le(L_);
+        if (mode_.dual)
+            for (int l = 0; l < L_; ++l)
+                le[l] = {NewEdge(k), NewEdge(k), NewEdge(k), NewEdge(k), NewEdge(k), NewEdge(k)};
+        if (mode_.flags) {
+            ctrl_.Alloc(std::max<size_t>(ctrl_blocks_, 1) * kWords * 4);
+            Check(hipMemset(ctrl_.get(), 0, ctrl_.bytes()), "zero ctrl");
+        }
+        const int rows_tile = S / k;
+        const int cgrid = mode_.split ? relay_grid_ : 0;
+        const int ctile = mode_.split ? rows_tile : 0;
+
+        // Consumer-side wait on a producer edge: in-kernel per tile (split),
+        // else a whole-edge wait ahead of the consumer.
+        auto consumer_wait = [&](int edge) -> RelayWait {
+            if (!mode_.dual) return RelayWait{};
+            if (mode_.split) {
+                for (int t = 0; t < k; ++t) consumed_.push_back(edge + t);
+                return WaitDesc(edge, k);
+            }
+            WaitBefore(C, edge, 1);
+            return RelayWait{};
+        };
+        auto release = [&](int edge) { return mode_.dual ? Pub(edge, rows_tile) : RelayPub{}; };
+        auto after = [&](int s, int edge) {
+            if (mode_.dual && !mode_.flags) PublishAfter(s, edge);
+        };
+
+        uint16_t *h0 = h_[0].as<uint16_t>(), *h1 = h_[1].as<uint16_t>();
+        uint16_t *x = x_.as<uint16_t>();
+        {
+            const void *tab = embed_;
+            const int64_t *ids = ids_.as<int64_t>();
+            const int H = H_;
+            const int64_t V = V_;
+            Emit(P, [=](hipStream_t st) { EmbedLaunch(tab, ids, h0, S, H, V, st); });
+            RmsNorm(P, h0, layers_[0].ln1, x, S, H_, 1, 0);
+        }
+        uint16_t *hcur = h0, *hnxt = h1;
+        const int64_t ld = ldqkv_;
+        for (int l = 0; l < L_; ++l) {
+            const Layer &w = layers_[l];
+            if (mode_.dual && l > 0) WaitBefore(P, le[l - 1].exit, k);
+            uint16_t *qkv = qkv_.as<uint16_t>();
+            Gemm(P, x, H_, w.qkv, int(ld), H_, qkv, ld, w.bias, S, RelayPub{});
+            uint16_t *q = qkv, *kk = qkv + size_t(HQ_) * D_, *v = qkv + size_t(HQ_ + HKV_) * D_;
+            int64_t ldq = ld, ldk = ld;
+            if (qk_norm_) {
+                RmsNorm(P, q, w.qn, qn_.get(), S * HQ_, D_, HQ_, ld);
+                RmsNorm(P, kk, w.kn, kn_.get(), S * HKV_, D_, HKV_, ld);
+                q = qn_.as<uint16_t>();
+                kk = kn_.as<uint16_t>();
+                ldq = int64_t(HQ_) * D_;
+                ldk = int64_t(HKV_) * D_;
+            }
+            {
+                const int HQ = HQ_, HKV = HKV_, D = D_;
+                const uint16_t *cs = cos_, *sn = sin_;
+                Emit(P, [=](hipStream_t st) {
+                    RopeLaunch(kBF16, q, ldq, S, HQ, D, cs, sn, st);
+                    RopeLaunch(kBF16, kk, ldk, S, HKV, D, cs, sn, st);
+                });
+                uint16_t *attn = attn_.as<uint16_t>();
+                const float scale = float(1.0 / std::sqrt(double(D_)));
+                Emit(P, [=](hipStream_t st) {
+                    AttnLaunch(kBF16, q, ldq, kk, ldk, v, ld, attn, int64_t(HQ) * D, S, HQ, HKV, D, scale, st);
+                });
+            }
+            // o_proj -> Add+RMSNorm(post_attention_layernorm)
+            Gemm(P, attn_.get(), int64_t(HQ_) * D_, w.o, H_, HQ_ * D_, o_.get(), H_, nullptr, S,
+                 release(le[l].o_ln2));
+            after(P, le[l].o_ln2);
+            AddRmsNorm(C, hcur, o_.get(), w.ln2, x, hnxt, consumer_wait(le[l].o_ln2), ctile, release(le[l].ln2_gu),
+                       cgrid);
+            after(C, le[l].ln2_gu);
+            // gate/up -> SwiGLU
+            WaitBefore(P, le[l].ln2_gu, k);
+            Gemm(P, x, H_, w.gu, 2 * I_, H_, gu_.get(), 2 * int64_t(I_), nullptr, S, release(le[l].gu_act));
+            after(P, le[l].gu_act);
+            {
+                EwDesc e;
+                e.op = kEwSwigluGU;
+                e.x0 = gu_.get();
+                e.y = act_.get();
+                e.rows = S;
+                e.cols = I_;
+                e.tile_rows = ctile;
+                e.grid = cgrid;
+                e.wait = consumer_wait(le[l].gu_act);
+                e.pub = release(le[l].act_down);
+                Emit(C, [e](hipStream_t st) { EwLaunch(e, st); });
+                after(C, le[l].act_down);
+            }
+            // down -> Add+RMSNorm(next input_layernorm | final norm)
+            WaitBefore(P, le[l].act_down, k);
+            Gemm(P, act_.get(), I_, w.down, H_, I_, down_.get(), H_, nullptr, S, release(le[l].down_ln));
+            after(P, le[l].down_ln);
+            const RelayWait wd = consumer_wait(le[l].down_ln);
+            if (l + 1 < L_) {
+                AddRmsNorm(C, hnxt, down_.get(), layers_[l + 1].ln1, x, hcur, wd, ctile, release(le[l].exit), cgrid);
+            } else {
+                AddRmsNorm(C, hnxt, down_.get(), final_norm_, xf_.get(), hf_.get(), wd, ctile, release(le[l].exit),
+                           cgrid);
+            }
+            after(C, le[l].exit);
+        }
+        if (mode_.dual) WaitBefore(P, le[L_ - 1].exit, k);
+        Gemm(P, xf_.get(), H_, lm_, V_, H_, logits_.get(), V_, nullptr, S, RelayPub{});
+    }
+
+    void Capture()
+    {
+        Check(hipDeviceSynchronize(), "pre capture sync");
+        const int nstreams = mode_.dual ? 2 : 1;
+        graphs_.assign(2, {nullptr, nullptr});
+        for (int s = 0; s < nstreams; ++s) {
+            hipStream_t st = Stream(s);
+            hipGraph_t g = nullptr;
+            Check(hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal), "begin capture");
+            for (auto &it : prog_)
+                if (it.stream == s) it.fn(st);
+            Check(hipStreamEndCapture(st, &g), "end capture");
+            hipGraphExec_t ex = nullptr;
+            Check(hipGraphInstantiate(&ex, g, nullptr, nullptr, 0), "instantiate");
+            graphs_[s] = {g, ex};
+        }
+    }
+
+    struct Layer {
+        uint16_t *qkv, *bias, *o, *gu, *down, *ln1, *ln2, *qn, *kn;
+    };
+
+    std::string dir_;
+    int seq_;
+    int device_;
+    Mode mode_;
+    int H_ = 0, I_ = 0, L_ = 0, HQ_ = 0, HKV_ = 0, D_ = 0, V_ = 0, max_pos_ = 4096;
+    double eps_ = 1e-6;
+    bool qk_norm_ = false, qkv_bias_ = false;
+    int64_t ldqkv_ = 0;
+    std::map<std::string, TensorInfo> tensors_;
+    int fd_ = -1;
+    void *map_ = nullptr;
+    size_t map_bytes_ = 0;
+    DevBuf wbuf_;
+    size_t wcursor_ = 0;
+    std::vector<Layer> layers_;
+    uint16_t *embed_ = nullptr, *lm_ = nullptr, *final_norm_ = nullptr, *cos_ = nullptr, *sin_ = nullptr;
+    DevBuf ids_, h_[2], x_, qkv_, qn_, kn_, attn_, o_, gu_, act_, down_, hf_, xf_, logits_, rstd_;
+    StreamPair streams_;
+    std::vector<Item> prog_;
+    std::vector<std::pair<hipGraph_t, hipGraphExec_t>> graphs_;
+    DevBuf ctrl_;
+    size_t ctrl_blocks_ = 0;
+    std::vector<int> consumed_;
+    std::map<int, hipEvent_t> edge_event_;
+    std::vector<hipEvent_t> events_;
+    int relay_grid_ = 64;
+    uint32_t max_spins_ = kDefaultMaxSpins;
+    hipEvent_t t0_ = nullptr, tp_ = nullptr, tc_ = nullptr;
+    std::vector<double> samples_, host_samples_, dev_samples_;
+    int argmax_ = -1, ref_argmax_ = -1, flag_edges_ = 0, flag_timeouts_ = 0;
+    double maxdiff_ = -1.0, absmean_ = 0.0, margin_ = 0.0, load_ms_ = 0.0;
+    uint64_t fnv_ = 0;
+};
+
+// k row-slices of one op, captured into one graph and replayed (reference
+// ProfileMany, exec/qwen_main.cpp:1535-1783; same result schema :1760-1781).
+std::string Model::ProfileMany(const std::string &spec_path)
+{
+    const Value spec = json::ParseFile(spec_path);
+    const int rows = seq_;
+    hipStream_t st = streams_.prod;
+    std::vector<std::string> cases;
+    const Layer &w = layers_.at(0);
+    const int64_t ld = ldqkv_;
+    for (const auto &c : spec.At("cases").Items()) {
+        const std::string op = c.Str("op");
+        const int k = int(c.Num("k", 1));
+        if (k < 1 || rows % k != 0) continue;
+        const int per = rows / k;
+        std::vector<std::function<void(hipStream_t)>> calls;
+        std::string shape;
+        auto rowsl = [&](const DevBuf &b, int i, int64_t cols) {
+            return static_cast<void *>(b.as<uint16_t>() + size_t(i) * per * cols);
+        };
+        try {
+            if (op.rfind("matmul_", 0) == 0) {
+                const void *A = x_.get();
+                int64_t K = H_, N = H_, lda = H_;
+                const uint16_t *Bt = nullptr;
+                const DevBuf *Cb = &o_;
+                int64_t ldc = H_;
+                if (op == "matmul_q") {
+                    Bt = w.qkv; N = int64_t(HQ_) * D_; Cb = &qkv_; ldc = ld;
+                } else if (op == "matmul_k") {
+                    Bt = w.qkv + size_t(HQ_) * D_ * H_; N = int64_t(HKV_) * D_; Cb = &qkv_; ldc = ld;
+                } else if (op == "matmul_v") {
+                    Bt = w.qkv + size_t(HQ_ + HKV_) * D_ * H_; N = int64_t(HKV_) * D_; Cb = &qkv_; ldc = ld;
+                } else if (op == "matmul_qkv") {
+                    Bt = w.qkv; N = ld; Cb = &qkv_; ldc = ld;
+                } else if (op == "matmul_o") {
+                    A = attn_.get(); lda = int64_t(HQ_) * D_; K = lda; Bt = w.o; N = H_; Cb = &o_;
+                } else if (op == "matmul_gate" || op == "matmul_up") {
+                    // the fused gate/up projection stores gate and up interleaved;
+                    // its first I rows are an [I, H] operand of the same shape
+                    // (and cost) as either projection alone
+                    Bt = w.gu; N = I_; Cb = &gu_; ldc = 2 * int64_t(I_);
+                } else if (op == "matmul_gate_up") {
+                    Bt = w.gu; N = 2 * int64_t(I_); Cb = &gu_; ldc = N;
+                } else if (op == "matmul_down") {
+                    A = act_.get(); lda = I_; K = I_; Bt = w.down; N = H_; Cb = &down_;
+                } else if (op == "matmul_lm") {
+                    A = xf_.get(); Bt = lm_; N = V_; Cb = &logits_; ldc = V_;
+                } else {
+                    continue;
+                }
+                shape = "matmul|" + std::to_string(rows) + "x" + std::to_string(K) + "x" + std::to_string(N);
+                for (int i = 0; i < k; ++i) {
+                    GemmDesc d;
+                    d.dtype = kBF16;
+                    d.A = static_cast<const uint16_t *>(A) + size_t(i) * per * lda;
+                    d.lda = lda;
+                    d.Bt = Bt;
+                    d.ldb = K;
+                    d.C = Cb->as<uint16_t>() + size_t(i) * per * ldc;
+                    d.ldc = ldc;
+                    d.M = per;
+                    d.N = int(N);
+                    d.K = int(K);
+                    calls.push_back([d](hipStream_t s) { GemmLaunch(d, s); });
+                }
+            } else if (op == "add" || op == "mul" || op == "silu" || op == "swiglu") {
+                const bool wide = op != "add";
+                const int cols = wide ? I_ : H_;
+                shape = op + "|" + std::to_string(rows) + "x" + std::to_string(cols);
+                for (int i = 0; i < k; ++i) {
+                    EwDesc e;
+                    e.op = op == "add" ? kEwAdd : op == "mul" ? kEwMul : op == "silu" ? kEwSilu : kEwSwigluGU;
+                    e.rows = per;
+                    e.cols = cols;
+                    if (op == "add") {
+                        e.x0 = rowsl(h_[0], i, H_);
+                        e.x1 = rowsl(o_, i, H_);
+                        e.y = rowsl(h_[1], i, H_);
+                    } else if (op == "swiglu") {
+                        e.x0 = rowsl(gu_, i, 2 * int64_t(I_));
+                        e.y = rowsl(act_, i, I_);
+                    } else {
+                        e.x0 = rowsl(act_, i, I_);
+                        e.x1 = gu_.as<uint16_t>() + size_t(i) * per * I_;  // any [per, I] operand
+                        e.y = rowsl(act_, i, I_);
+                    }
+                    calls.push_back([e](hipStream_t s) { EwLaunch(e, s); });
+                }
+            } else if (op == "rmsnorm" || op == "add_rmsnorm") {
+                shape = op + "|" + std::to_string(rows) + "x" + std::to_string(H_);
+                for (int i = 0; i < k; ++i) {
+                    RowDesc d;
+                    d.op = op == "rmsnorm" ? kRowRmsNorm : kRowAddRmsNorm;
+                    d.x0 = rowsl(h_[0], i, H_);
+                    d.x1 = rowsl(o_, i, H_);
+                    d.gamma = w.ln2;
+                    d.y = rowsl(x_, i, H_);
+                    d.sum_out = op == "add_rmsnorm" ? rowsl(h_[1], i, H_) : nullptr;
+                    d.rstd_out = rstd_.as<float>() + size_t(i) * per;
+                    d.rows = per;
+                    d.cols = H_;
+                    d.eps = float(eps_);
+                    calls.push_back([d](hipStream_t s) { RowLaunch(d, s); });
+                }
+            } else if (op == "rope") {
+                shape = "rope|" + std::to_string(rows) + "x" + std::to_string((HQ_ + HKV_) * D_);
+                for (int i = 0; i < k; ++i) {
+                    uint16_t *q = qkv_.as<uint16_t>() + size_t(i) * per * ld;
+                    uint16_t *kk = q + size_t(HQ_) * D_;
+                    const uint16_t *cs = cos_ + size_t(i) * per * D_, *sn = sin_ + size_t(i) * per * D_;
+                    const int HQ = HQ_, HKV = HKV_, D = D_;
+                    calls.push_back([=](hipStream_t s) {
+                        RopeLaunch(kBF16, q, ld, per, HQ, D, cs, sn, s);
+                        RopeLaunch(kBF16, kk, ld, per, HKV, D, cs, sn, s);
+                    });
+                }
+            } else if (op == "embedding") {
+                shape = "embedding|" + std::to_string(rows) + "x" + std::to_string(H_);
+                for (int i = 0; i < k; ++i) {
+                    const int64_t *ids = ids_.as<int64_t>() + size_t(i) * per;
+                    void *out = rowsl(h_[0], i, H_);
+                    const void *tab = embed_;
+                    const int H = H_;
+                    const int64_t V = V_;
+                    calls.push_back([=](hipStream_t s) { EmbedLaunch(tab, ids, out, per, H, V, s); });
+                }
+            } else if (op == "attention") {
+                if (HQ_ % k != 0) continue;
+                const int hq = HQ_ / k;
+                const bool kv_div = HKV_ % k == 0;
+                const int hkv = kv_div ? HKV_ / k : 1;
+                if (hq % hkv != 0) continue;
+                shape = "attention|" + std::to_string(HQ_) + "x" + std::to_string(rows) + "x" + std::to_string(D_);
+                const float scale = float(1.0 / std::sqrt(double(D_)));
+                for (int g = 0; g < k; ++g) {
+                    // k > HKV: one KV head per group, cycled over the HKV heads
+                    // (the reference's E1 GQA replication, qwen_main.cpp:1690-1696)
+                    const int kv_off = kv_div ? g * hkv : g % HKV_;
+                    const uint16_t *q = qkv_.as<uint16_t>() + size_t(g) * hq * D_;
+                    const uint16_t *kk = qkv_.as<uint16_t>() + size_t(HQ_ + kv_off) * D_;
+                    const uint16_t *v = qkv_.as<uint16_t>() + size_t(HQ_ + HKV_ + kv_off) * D_;
+                    uint16_t *o = attn_.as<uint16_t>() + size_t(g) * hq * D_;
+                    const int D = D_;
+                    const int64_t ldo = int64_t(HQ_) * D_;
+                    calls.push_back([=](hipStream_t s) {
+                        AttnLaunch(kBF16, q, ld, kk, ld, v, ld, o, ldo, rows, hq, hkv, D, scale, s);
+                    });
+                }
+            } else {
+                continue;
+            }
+        } catch (const std::exception &e) {
+            Value err = Value::MakeObject();
+            err.Set("op", Value::MakeString(op));
+            err.Set("k", Value::MakeNumber(k));
+            err.Set("error", Value::MakeString(e.what()));
+            cases.push_back(err.Dump());
+            continue;
+        }
+        hipGraph_t graph = nullptr;
+        hipGraphExec_t exec = nullptr;
+        Check(hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal), "profile capture");
+        for (auto &f : calls) f(st);
+        Check(hipStreamEndCapture(st, &graph), "profile capture end");
+        Check(hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0), "profile instantiate");
+        const int repeats = 20;
+        for (int i = 0; i < 2; ++i) {
+            Check(hipGraphLaunch(exec, st), "profile warmup");
+            Check(hipStreamSynchronize(st), "profile warmup sync");
+        }
+        hipEvent_t e0 = nullptr, e1 = nullptr;
+        Check(hipEventCreate(&e0), "event");
+        Check(hipEventCreate(&e1), "event");
+        std::vector<double> dev, wall, host;
+        for (int it = 0; it < 3; ++it) {
+            Check(hipEventRecord(e0, st), "record");
+            const auto t0 = Clock::now();
+            for (int r = 0; r < repeats; ++r) Check(hipGraphLaunch(exec, st), "profile replay");
+            const auto te = Clock::now();
+            Check(hipEventRecord(e1, st), "record");
+            Check(hipStreamSynchronize(st), "profile sync");
+            const auto t1 = Clock::now();
+            float ms = 0.f;
+            Check(hipEventElapsedTime(&ms, e0, e1), "elapsed");
+            dev.push_back(double(ms) * 1000.0 / repeats);
+            host.push_back(Us(t0, te) / repeats);
+            wall.push_back(Us(t0, t1) / repeats);
+        }
+        (void)hipEventDestroy(e0);
+        (void)hipEventDestroy(e1);
+        (void)hipGraphExecDestroy(exec);
+        (void)hipGraphDestroy(graph);
+        Value r = Value::MakeObject();
+        r.Set("op", Value::MakeString(op));
+        r.Set("k", Value::MakeNumber(k));
+        r.Set("rows", Value::MakeNumber(rows));
+        r.Set("shape", Value::MakeString(shape));
+        r.Set("best_us", Value::MakeNumber(Min(dev)));
+        r.Set("median_us", Value::MakeNumber(Median(dev)));
+        r.Set("per_tile_us", Value::MakeNumber(Min(dev) / k));
+        r.Set("wall_best_us", Value::MakeNumber(Min(wall)));
+        r.Set("host_enqueue_us", Value::MakeNumber(Min(host)));
+        r.Set("graph", Value::MakeBool(true));
+        Value sa = Value::MakeArray();
+        for (double d : dev) sa.Push(Value::MakeNumber(d));
+        r.Set("samples_us", sa);
+        cases.push_back(r.Dump());
+    }
+    std::ostringstream out;
+    out <<"{\"model\":" << Value::MakeString(dir_).Dump() << ",\"cases\":[";
+    for (size_t i = 0; i < cases.size(); ++i) out << (i ? "," : "") << cases[i];
+    out << "]}";
+    return out.str();
+}
+
+int CopyOut(const std::string &res, char *out, size_t cap)
+{
+    if (out == nullptr || cap < res.size() + 1) throw std::runtime_error("output buffer too small");
+    std::memcpy(out, res.c_str(), res.size() + 1);
+    return 0;
+}
+
+int Fail(const std::exception &e, char *out, size_t cap)
+{
+    if (out != nullptr && cap > 0) {
+        Value v = Value::MakeObject();
+        v.Set("error", Value::MakeString(e.what()));
+        std::snprintf(out, cap, "%s", v.Dump().c_str());
+    }
+    return 1;
+}
+
+}  // namespace qwen
+}  // namespace kr
+
+extern "C" int kr_qwen_run(const char *model_dir, const char *mode, int seq, int device, int warmup, int iters,
+                           char *out, size_t out_cap)
+{
+    try {
+        if (model_dir == nullptr || *model_dir == '\0') throw std::runtime_error("model path required");
+        if (iters < 1 || warmup < 0) throw std::runtime_error("iters must be >= 1 and warmup >= 0");
+        std::string res;
+        {
+            kr::qwen::Model m(model_dir, seq, device, mode ? mode : "serial_graph");
+            m.Build();
+            m.RunOnce();
+            kr::Check(hipDeviceSynchronize(), "first sync");
+            m.Verify();
+            m.Bench(warmup, iters);
+            m.Verify();  // recheck numerics and flag status after the replays
+            res = m.ResultJson(warmup, iters);
+        }
+        return kr::qwen::CopyOut(res, out, out_cap);
+    } catch (const std::exception &e) {
+        return kr::qwen::Fail(e, out, out_cap);
+    }
+}
+
+extern "C" int kr_qwen_profile_many(const char *model_dir, const char *spec_json, int seq, int device, char *out,
+                                    size_t out_cap)
+{
+    try {
+        if (model_dir == nullptr || *model_dir == '\0') throw std::runtime_error("model path required");
+        if (spec_json == nullptr) throw std::runtime_error("spec path required");
+        std::string res;
+        {
+            kr::qwen::Model m(model_dir, seq, device, "serial");
+            m.Build(false);
+            res = m.ProfileMany(spec_json);
+        }
+        return kr::qwen::CopyOut(res, out, out_cap);
+    } catch (const std::exception &e) {
+        return kr::qwen::Fail(e, out, out_cap);
+    }
+}
+
+extern "C" int kr_qwen_pp_run(const char *, const char *, int, int, int, int, int, int, char *out, size_t out_cap)
+{
+    return kr::qwen::Fail(std::runtime_error("multi-GPU not in scope"), out, out_cap);
+}
+
+extern "C" int kr_qwen_tp_run(const char *, const char *, int, int, int, int, int, int, char *out, size_t out_cap)
+{
+    return kr::qwen::Fail(std::runtime_error("multi-GPU not in scope"), out, out_cap);
+}
+
+extern "C" const char *kr_version(void) { return "KernRelay-MI355X 0.1 (libkernrelay, gfx950)"; }

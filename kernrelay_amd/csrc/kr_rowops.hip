@@ -1,0 +1,394 @@
+// Consumer kernels: elementwise and row-reduction ops with the relay
+// prologue (wait on the producer tiles that cover a tile's rows) and
+// epilogue (release the tile to the next consumer).
+//
+// Replaces the reference's aclnnGelu / aclnnSoftmax(dim=1) / aclnnCast
+// (exec/runtime/op_impl.cpp:214-233), aclnnSilu + aclnnMul
+// (exec/qwen_main.cpp:616-644), aclnnAdd (:514-529), aclnnRmsNorm (:531-546)
+// and aclnnAddRmsNorm (:548-565).
+//
+// Work is walked tile by tile (tile = tile_rows rows). Every workgroup waits
+// for tile t, processes its share of tile t with a grid stride, arrives on
+// tile t's release, then moves on: with a bounded grid the kernel is a
+// persistent consumer whose spinning workgroups can never occupy more than
+// `grid` slots, so the producer always keeps CUs to make progress.
+//
+// Arithmetic is in fp32 with one rounding per stored tensor, matching the
+// storage rounding of the reference's op sequence. Row reductions use a fixed
+// tree (per-lane serial, then xor-butterfly, then waves in index order) that
+// depends only on `cols`, never on the tiling, so split == unsplit bit-exact.
+#include "kr_rowops.h"
+
+#include <algorithm>
+
+namespace kr {
+
+namespace {
+
+constexpr int kThreads = 256;
+
+// ----------------------------------------------------------------- elementwise
+struct EwParams {
+    const uint16_t *x0;
+    const uint16_t *x1;
+    void *y;
+    int64_t tile_chunks;
+    int64_t total_chunks;
+    int rows, tile_rows, n_tiles;
+    RelayWait w;
+    RelayPub pub;
+};
+
+__device__ __forceinline__ float GeluTanh(float x)
+{
+    const float k0 = 0.7978845608028654f;  // sqrt(2/pi)
+    const float k1 = 0.044715f;
+    return 0.5f * x * (1.0f + tanhf(k0 * (x + k1 * x * x * x)));
+}
+
+__device__ __forceinline__ float Silu(float x) { return x / (1.0f + expf(-x)); }
+
+template <int OP, int DTI, int DTO>
+__global__ void __launch_bounds__(kThreads) EwKernel(EwParams p)
+{
+    const int64_t stride = int64_t(gridDim.x) * kThreads;
+    for (int t = 0; t < p.n_tiles; ++t) {
+        const int r_lo = t * p.tile_rows;
+        const int r_hi = min(r_lo + p.tile_rows, p.rows);
+        RelayWaitRows(p.w, r_lo, r_hi);
+        const int64_t c0 = int64_t(t) * p.tile_chunks;
+        const int64_t c1 = min(c0 + p.tile_chunks, p.total_chunks);
+        for (int64_t c = c0 + int64_t(blockIdx.x) * kThreads + threadIdx.x; c < c1; c += stride) {
+            U16x8 a, b;
+            if constexpr (OP == kEwSwigluGU) {
+                // fused gate/up rows: 8 gate columns then the matching 8 up columns
+                a = LoadU16x8(p.x0 + c * 16);
+                b = LoadU16x8(p.x0 + c * 16 + 8);
+            } else {
+                a = LoadU16x8(p.x0 + c * 8);
+                if constexpr (OP == kEwMul || OP == kEwAdd || OP == kEwSwiglu) b = LoadU16x8(p.x1 + c * 8);
+            }
+            float o[8];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const float x = Elem<DTI>::Load(a.v[e]);
+                if constexpr (OP == kEwGelu) {
+                    o[e] = GeluTanh(x);
+                } else if constexpr (OP == kEwSilu) {
+                    o[e] = Silu(x);
+                } else if constexpr (OP == kEwCast) {
+                    o[e] = x;
+                } else if constexpr (OP == kEwMul) {
+                    o[e] = x * Elem<DTI>::Load(b.v[e]);
+                } else if constexpr (OP == kEwAdd) {
+                    o[e] = x + Elem<DTI>::Load(b.v[e]);
+                } else {  // swiglu: the silu result is stored (rounded) before the multiply
+                    o[e] = RoundTo<DTI>(Silu(x)) * Elem<DTI>::Load(b.v[e]);
+                }
+            }
+            if constexpr (DTO == kF32) {
+                float4 *yp = reinterpret_cast<float4 *>(static_cast<float *>(p.y) + c * 8);
+                yp[0] = make_float4(o[0], o[1], o[2], o[3]);
+                yp[1] = make_float4(o[4], o[5], o[6], o[7]);
+            } else {
+                U16x8 r;
+#pragma unroll
+                for (int e = 0; e < 8; ++e) r.v[e] = Elem<DTO>::Store(o[e]);
+                StoreU16x8(static_cast<uint16_t *>(p.y) + c * 8, r);
+            }
+        }
+        RelayArrive(p.pub, t);
+    }
+    RelayFinish(p.w);
+}
+
+// ------------------------------------------------------------------ row ops
+struct RowParams {
+    const uint16_t *x0;
+    const uint16_t *x1;
+    const uint16_t *gamma;
+    uint16_t *y;
+    uint16_t *sum_out;
+    float *rstd_out;
+    int rows, cols, tile_rows, n_tiles;
+    int in_group;
+    int64_t in_ld;
+    float eps;
+    RelayWait w;
+    RelayPub pub;
+};
+
+// Sum / max over the LPR lanes that own one row. LPR == 256 crosses waves
+// through LDS; the caller guarantees the whole workgroup calls it together.
+template <int LPR, bool MAX>
+__device__ __forceinline__ float GroupReduce(float v, float *red)
+{
+    if constexpr (LPR <= 64) {
+#pragma unroll
+        for (int o = LPR / 2; o > 0; o >>= 1) {
+            const float u = __shfl_xor(v, o, 64);
+            v = MAX ? fmaxf(v, u) : v + u;
+        }
+        return v;
+    } else {
+        v = MAX ? WaveMax(v) : WaveSum(v);
+        __syncthreads();
+        if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+        __syncthreads();
+        if (MAX) return fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+        return ((red[0] + red[1]) + red[2]) + red[3];
+    }
+}
+
+template <int OP, int DT, int LPR, int CPL>
+__global__ void __launch_bounds__(kThreads) RowKernel(RowParams p)
+{
+    constexpr int RPB = kThreads / LPR;
+    __shared__ float red[4];
+    const int slot = threadIdx.x / LPR;
+    const int ln = threadIdx.x % LPR;
+    const int chunks = p.cols / 8;
+
+    for (int t = 0; t < p.n_tiles; ++t) {
+        const int r_lo = t * p.tile_rows;
+        const int r_hi = min(r_lo + p.tile_rows, p.rows);
+        RelayWaitRows(p.w, r_lo, r_hi);
+        for (int rb = r_lo + int(blockIdx.x) * RPB; rb < r_hi; rb += int(gridDim.x) * RPB) {
+            const int r = rb + slot;
+            const bool active = r < r_hi;
+            const int rr = active ? r : r_lo;
+            const int64_t base = int64_t(rr) * p.cols;
+            const int64_t ibase = int64_t(rr / p.in_group) * p.in_ld + int64_t(rr % p.in_group) * p.cols;
+            float v[CPL][8];
+            bool ok[CPL];
+#pragma unroll
+            for (int c = 0; c < CPL; ++c) {
+                const int ch = ln + c * LPR;
+                ok[c] = active && ch < chunks;
+                if (ok[c]) {
+                    const U16x8 a = LoadU16x8(p.x0 + ibase + ch * 8);
+                    if constexpr (OP == kRowAddRmsNorm) {
+                        const U16x8 b = LoadU16x8(p.x1 + ibase + ch * 8);
+                        U16x8 s;
+#pragma unroll
+                        for (int e = 0; e < 8; ++e) {
+                            s.v[e] = Elem<DT>::Store(Elem<DT>::Load(a.v[e]) + Elem<DT>::Load(b.v[e]));
+                            v[c][e] = Elem<DT>::Load(s.v[e]);
+                        }
+                        if (p.sum_out != nullptr) StoreU16x8(p.sum_out + base + ch * 8, s);
+                    } else {
+#pragma unroll
+                        for (int e = 0; e < 8; ++e) v[c][e] = Elem<DT>::Load(a.v[e]);
+                    }
+                } else {
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) v[c][e] = 0.0f;
+                }
+            }
+
+            if constexpr (OP == kRowSoftmax) {
+                float m = -INFINITY;
+#pragma unroll
+                for (int c = 0; c < CPL; ++c)
+                    if (ok[c])
+#pragma unroll
+                        for (int e = 0; e < 8; ++e) m = fmaxf(m, v[c][e]);
+                m = GroupReduce<LPR, true>(m, red);
+                float s = 0.0f;
+#pragma unroll
+                for (int c = 0; c < CPL; ++c)
+                    if (ok[c])
+#pragma unroll
+                        for (int e = 0; e < 8; ++e) {
+                            v[c][e] = expf(v[c][e] - m);
+                            s += v[c][e];
+                        }
+                s = GroupReduce<LPR, false>(s, red);
+#pragma unroll
+                for (int c = 0; c < CPL; ++c) {
+                    if (!ok[c]) continue;
+                    U16x8 o;
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) o.v[e] = Elem<DT>::Store(v[c][e] / s);
+                    StoreU16x8(p.y + base + (ln + c * LPR) * 8, o);
+                }
+            } else {
+                float ss = 0.0f;
+#pragma unroll
+                for (int c = 0; c < CPL; ++c)
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) ss += v[c][e] * v[c][e];
+                ss = GroupReduce<LPR, false>(ss, red);
+                const float rstd = 1.0f / sqrtf(ss / float(p.cols) + p.eps);
+                if (p.rstd_out != nullptr && active && ln == 0) p.rstd_out[r] = rstd;
+#pragma unroll
+                for (int c = 0; c < CPL; ++c) {
+                    if (!ok[c]) continue;
+                    const int ch = ln + c * LPR;
+                    const U16x8 g = LoadU16x8(p.gamma + ch * 8);
+                    U16x8 o;
+#pragma unroll
+                    for (int e = 0; e < 8; ++e)
+                        o.v[e] = Elem<DT>::Store(Elem<DT>::Load(g.v[e]) * RoundTo<DT>(v[c][e] * rstd));
+                    StoreU16x8(p.y + base + ch * 8, o);
+                }
+            }
+        }
+        RelayArrive(p.pub, t);
+    }
+    RelayFinish(p.w);
+}
+
+__global__ void __launch_bounds__(64) WaitKernel(RelayWait w, int lo, int hi)
+{
+    RelayWaitRows(w, lo, hi);
+    RelayFinish(w);
+}
+
+__global__ void __launch_bounds__(64) PublishKernel(RelayPub p, int tile) { RelayArrive(p, tile); }
+
+int TileCount(int rows, int tile_rows) { return (rows + tile_rows - 1) / tile_rows; }
+
+template <int OP>
+void EwDispatch(const EwDesc &d, const EwParams &p, int grid, hipStream_t s)
+{
+    auto go = [&](auto kern) { hipLaunchKernelGGL(kern, dim3(grid), dim3(kThreads), 0, s, p); };
+    if (OP == kEwCast) {
+        if (d.dtype_in == kBF16 && d.dtype_out == kF16) return go(EwKernel<kEwCast, kBF16, kF16>);
+        if (d.dtype_in == kBF16 && d.dtype_out == kF32) return go(EwKernel<kEwCast, kBF16, kF32>);
+        if (d.dtype_in == kF16 && d.dtype_out == kF32) return go(EwKernel<kEwCast, kF16, kF32>);
+        if (d.dtype_in == kF16 && d.dtype_out == kBF16) return go(EwKernel<kEwCast, kF16, kBF16>);
+        throw std::runtime_error("cast: unsupported dtype pair");
+    }
+    if (d.dtype_in != d.dtype_out) throw std::runtime_error("elementwise: dtype_in != dtype_out");
+    if (d.dtype_in == kBF16) return go(EwKernel<OP, kBF16, kBF16>);
+    if (d.dtype_in == kF16) return go(EwKernel<OP, kF16, kF16>);
+    throw std::runtime_error("elementwise: dtype must be bf16 or f16");
+}
+
+template <int OP, int DT>
+void RowDispatchT(const RowParams &p, int lpr, int cpl, int grid, hipStream_t s)
+{
+    auto go = [&](auto kern) { hipLaunchKernelGGL(kern, dim3(grid), dim3(kThreads), 0, s, p); };
+    if (lpr == 16) return go(RowKernel<OP, DT, 16, 1>);
+    if (lpr == 64) return go(RowKernel<OP, DT, 64, 1>);
+    switch (cpl) {
+        case 1: return go(RowKernel<OP, DT, 256, 1>);
+        case 2: return go(RowKernel<OP, DT, 256, 2>);
+        case 4: return go(RowKernel<OP, DT, 256, 4>);
+        default: return go(RowKernel<OP, DT, 256, 8>);
+    }
+}
+
+template <int OP>
+void RowDispatch(const RowDesc &d, const RowParams &p, int lpr, int cpl, int grid, hipStream_t s)
+{
+    if (d.dtype == kBF16) return RowDispatchT<OP, kBF16>(p, lpr, cpl, grid, s);
+    if (d.dtype == kF16) return RowDispatchT<OP, kF16>(p, lpr, cpl, grid, s);
+    throw std::runtime_error("row op: dtype must be bf16 or f16");
+}
+
+void CheckAligned(const void *p, const char *what)
+{
+    if (reinterpret_cast<uintptr_t>(p) & 15) throw std::runtime_error(std::string(what) + " must be 16-byte aligned");
+}
+
+}  // namespace
+
+void EwLaunch(const EwDesc &d, hipStream_t stream)
+{
+    if (d.rows <= 0 || d.cols <= 0) return;
+    if (d.cols % 8 != 0) throw std::runtime_error("elementwise: cols must be a multiple of 8");
+    CheckAligned(d.x0, "elementwise x0");
+    CheckAligned(d.y, "elementwise y");
+    const bool binary = d.op == kEwMul || d.op == kEwAdd || d.op == kEwSwiglu;
+    if (binary) CheckAligned(d.x1, "elementwise x1");
+    EwParams p{};
+    p.x0 = static_cast<const uint16_t *>(d.x0);
+    p.x1 = static_cast<const uint16_t *>(d.x1);
+    p.y = d.y;
+    p.rows = d.rows;
+    p.tile_rows = d.tile_rows > 0 ? d.tile_rows : d.rows;
+    p.n_tiles = TileCount(d.rows, p.tile_rows);
+    p.tile_chunks = int64_t(p.tile_rows) * d.cols / 8;
+    p.total_chunks = int64_t(d.rows) * d.cols / 8;
+    p.w = d.wait;
+    p.pub = d.pub;
+    int grid = d.grid;
+    if (grid <= 0) {
+        const int64_t want = (p.tile_chunks + kThreads - 1) / kThreads;
+        grid = int(std::min<int64_t>(std::max<int64_t>(want, 1), 4096));
+    }
+    p.pub.arrivals = grid;
+    switch (d.op) {
+        case kEwGelu: return EwDispatch<kEwGelu>(d, p, grid, stream);
+        case kEwSilu: return EwDispatch<kEwSilu>(d, p, grid, stream);
+        case kEwCast: return EwDispatch<kEwCast>(d, p, grid, stream);
+        case kEwMul: return EwDispatch<kEwMul>(d, p, grid, stream);
+        case kEwAdd: return EwDispatch<kEwAdd>(d, p, grid, stream);
+        case kEwSwiglu: return EwDispatch<kEwSwiglu>(d, p, grid, stream);
+        case kEwSwigluGU: return EwDispatch<kEwSwigluGU>(d, p, grid, stream);
+        default: throw std::runtime_error("elementwise: unknown op");
+    }
+}
+
+void RowLaunch(const RowDesc &d, hipStream_t stream)
+{
+    if (d.rows <= 0 || d.cols <= 0) return;
+    if (d.cols % 8 != 0) throw std::runtime_error("row op: cols must be a multiple of 8");
+    if (d.cols > 16384) throw std::runtime_error("row op: cols must be <= 16384");
+    CheckAligned(d.x0, "row op x0");
+    CheckAligned(d.y, "row op y");
+    if (d.op == kRowAddRmsNorm) CheckAligned(d.x1, "add_rmsnorm x1");
+    if (d.op != kRowSoftmax) CheckAligned(d.gamma, "rmsnorm gamma");
+    if (d.sum_out) CheckAligned(d.sum_out, "add_rmsnorm sum");
+    RowParams p{};
+    p.x0 = static_cast<const uint16_t *>(d.x0);
+    p.x1 = static_cast<const uint16_t *>(d.x1);
+    p.gamma = static_cast<const uint16_t *>(d.gamma);
+    p.y = static_cast<uint16_t *>(d.y);
+    p.sum_out = static_cast<uint16_t *>(d.sum_out);
+    p.rstd_out = d.rstd_out;
+    p.rows = d.rows;
+    p.cols = d.cols;
+    p.in_group = d.in_group > 0 ? d.in_group : 1;
+    p.in_ld = d.in_ld > 0 ? d.in_ld : int64_t(d.cols) * p.in_group;
+    if (p.in_ld % 8 != 0) throw std::runtime_error("row op: in_ld must be a multiple of 8");
+    p.eps = d.eps;
+    p.tile_rows = d.tile_rows > 0 ? d.tile_rows : d.rows;
+    p.n_tiles = TileCount(d.rows, p.tile_rows);
+    p.w = d.wait;
+    p.pub = d.pub;
+    const int chunks = d.cols / 8;
+    const int lpr = chunks <= 16 ? 16 : (chunks <= 64 ? 64 : 256);
+    int cpl = (chunks + lpr - 1) / lpr;
+    cpl = cpl <= 1 ? 1 : (cpl <= 2 ? 2 : (cpl <= 4 ? 4 : 8));
+    const int rpb = kThreads / lpr;
+    int grid = d.grid;
+    if (grid <= 0) grid = std::max(1, std::min((p.tile_rows + rpb - 1) / rpb, 8192));
+    p.pub.arrivals = grid;
+    switch (d.op) {
+        case kRowSoftmax: return RowDispatch<kRowSoftmax>(d, p, lpr, cpl, grid, stream);
+        case kRowRmsNorm: return RowDispatch<kRowRmsNorm>(d, p, lpr, cpl, grid, stream);
+        case kRowAddRmsNorm: return RowDispatch<kRowAddRmsNorm>(d, p, lpr, cpl, grid, stream);
+        default: throw std::runtime_error("row op: unknown op");
+    }
+}
+
+void WaitLaunch(const RelayWait &w, int lo, int hi, hipStream_t stream)
+{
+    if (w.ctrl == nullptr) return;
+    hipLaunchKernelGGL(WaitKernel, dim3(1), dim3(64), 0, stream, w, lo, hi);
+    Check(hipGetLastError(), "wait launch");
+}
+
+void PublishLaunch(const RelayPub &p, int tile, hipStream_t stream)
+{
+    if (p.ctrl == nullptr) return;
+    RelayPub q = p;
+    q.arrivals = 1;
+    hipLaunchKernelGGL(PublishKernel, dim3(1), dim3(64), 0, stream, q, tile);
+    Check(hipGetLastError(), "publish launch");
+}
+
+}  // namespace kr

@@ -1,0 +1,67 @@
+"""The mm -> consumer DAG workloads of the relay path, as DAG dicts plus
+seeded input files for kr_plan_run.
+
+* tiny mm->GELU: X[256,512] ~ N(0,1), W[512,512] ~ N(0,0.02), bf16, the
+  producer split into 2 row tiles (the reference's e0-style DAG,
+  dags/e0_tiny_mm_gelu.json, at the task's shapes and dtype);
+* mm fan-out: X[4096,4096] ~ N(0,1), W[4096,4096] ~ N(0,0.02), bf16; every
+  tile feeds row-softmax, GELU and a bf16->fp16 cast (the reference's 1:N
+  fan-out, dags/f04_mm_fanout_c2.json, with the cast consumer added).
+
+Inputs are written once per (shape, seed) as raw bf16 files: X as [M, K],
+W as the weight_t layout [K, N] the executor reads.
+"""
+
+from pathlib import Path
+
+import torch
+
+from . import schedule
+
+
+def write_inputs(out_dir, M, K, N, seed=1234, x_std=1.0, w_std=0.02):
+    out = Path(out_dir)
+    out.mkdir(parents=True, exist_ok=True)
+    g = torch.Generator().manual_seed(seed)
+    x = torch.empty(M, K).normal_(0.0, x_std, generator=g).to(torch.bfloat16)
+    w = torch.empty(K, N).normal_(0.0, w_std, generator=g).to(torch.bfloat16)
+    px, pw = out / ("x_%dx%d_s%d.bin" % (M, K, seed)), out / ("w_%dx%d_s%d.bin" % (K, N, seed))
+    x.view(torch.int16).numpy().tofile(px)
+    w.view(torch.int16).numpy().tofile(pw)
+    return {"in": str(px), "b": str(pw)}
+
+
+def mm_consumers_dag(name, M, K, N, consumers, dtype="bf16", inputs=None, cast_to="fp16"):
+    """DAG dict: one matmul feeding each consumer op in `consumers`."""
+    mm = {"name": "mm", "op": "matmul", "engine": "aic", "shape": {"M": M, "K": K, "N": N}, "dtype": dtype}
+    if inputs:
+        mm["inputs"] = dict(inputs)
+    nodes = [mm]
+    for op in consumers:
+        node = {"name": op, "op": op, "engine": "aiv", "shape": {"rows": M, "cols": N}, "dtype": dtype}
+        if op == "cast":
+            node["to"] = cast_to
+        nodes.append(node)
+    edges = [{"src": "mm", "dst": op, "kind": "data"} for op in consumers]
+    return {"name": name, "description": "mm -> %s" % ",".join(consumers), "nodes": nodes, "edges": edges}
+
+
+def tiny_mm_gelu(out_dir, seed=1234):
+    inputs = write_inputs(out_dir, 256, 512, 512, seed)
+    return schedule.dag_from_dict(mm_consumers_dag("tiny_mm_gelu", 256, 512, 512, ["gelu"], inputs=inputs))
+
+
+def mm_fanout(out_dir, M=4096, K=4096, N=4096, seed=1234, consumers=("softmax", "gelu", "cast")):
+    inputs = write_inputs(out_dir, M, K, N, seed)
+    return schedule.dag_from_dict(mm_consumers_dag("mm_fanout", M, K, N, list(consumers), inputs=inputs))
+
+
+def variants(dag, k, nranks=1):
+    """serial (one stream), B0 (two streams, unsplit) and split-at-k schedules
+    (the reference's E3/E4 variants, python/kernrelay/e34.py:16-22)."""
+    chunking = {n.name: k for n in dag.nodes}
+    return {
+        "serial": schedule.serial_schedule(dag, nranks=nranks),
+        "b0": schedule.build_fixed_schedule(dag, {}, nranks=nranks, method="B0-nosplit"),
+        "split": schedule.build_fixed_schedule(dag, chunking, nranks=nranks, method="KernRelay-split"),
+    }

@@ -1,0 +1,285 @@
+"""Op-level parity of the HIP kernels (through the C ABI) against the oracle.
+
+Tolerance for bf16 outputs: |gpu - oracle| <= 2e-2 + 1e-2 * |oracle|
+(the task's max-abs 2e-2 / relative 1e-2); integer, byte and copy work
+bit-exact; the relay split bit-exact against the unsplit kernel.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from kernrelay_amd import ops
+from oracle import ops as O
+from tests.conftest import announce
+
+pytestmark = pytest.mark.gpu
+
+ATOL, RTOL = 2e-2, 1e-2
+
+
+def close(gpu, ref, atol=ATOL, rtol=RTOL):
+    g = gpu.float().cpu()
+    r = ref.float().cpu()
+    err = (g - r).abs()
+    bound = atol + rtol * r.abs()
+    bad = err > bound
+    i = int((err - bound).flatten().argmax())
+    assert not bool(bad.any()), "max err %.4g at flat index %d (ref %.4g gpu %.4g), %d bad" % (
+        float(err.max()), i, float(r.flatten()[i]), float(g.flatten()[i]), int(bad.sum()))
+
+
+def rand(shape, std=1.0, seed=0, dt=torch.bfloat16):
+    g = torch.Generator().manual_seed(seed)
+    return (torch.randn(*shape, generator=g) * std).to(dt)
+
+
+@pytest.mark.parametrize("M,N,K", [(256, 512, 512), (100, 200, 72), (512, 640, 1024), (64, 1024, 4096),
+                                   (2048, 4608, 3584)])
+def test_gemm_matches_oracle(gpu, M, N, K):
+    announce("gemm %dx%dx%d" % (M, N, K))
+    A = rand((M, K), 1.0, 1)
+    W = rand((K, N), 0.02, 2)                       # weight_t layout [K, N]
+    ref = O.gemm(A.float(), W.float())
+    Bt = W.t().contiguous().cuda()
+    C = torch.empty(M, N, dtype=torch.bfloat16, device="cuda")
+    ops.gemm(A.cuda(), Bt, C)
+    torch.cuda.synchronize()
+    close(C, ref)
+
+
+def test_gemm_fp16_and_bias(gpu):
+    announce("gemm fp16 + bias")
+    M, N, K = 256, 384, 256
+    A = rand((M, K), 1.0, 3, torch.float16)
+    W = rand((K, N), 0.05, 4, torch.float16)
+    b = rand((N,), 0.5, 5, torch.float16)
+    ref = O.gemm(A.float(), W.float(), b.float(), dt=torch.float16)
+    C = torch.empty(M, N, dtype=torch.float16, device="cuda")
+    ops.gemm(A.cuda(), W.t().contiguous().cuda(), C, bias=b.cuda())
+    torch.cuda.synchronize()
+    close(C, ref)
+    # bias applied to the rounded product: exactly rnd(rnd(acc) + b) of the GPU's own acc
+    C0 = torch.empty_like(C)
+    ops.gemm(A.cuda(), W.t().contiguous().cuda(), C0)
+    torch.cuda.synchronize()
+    assert torch.equal(C.cpu(), (C0.cpu().float() + b.float()).to(torch.float16))
+
+
+def test_gemm_tiles_bit_exact(gpu):
+    """Every macro-tile shape runs the same MFMA and K order: identical bits."""
+    announce("gemm tile variants")
+    M, N, K = 512, 768, 1536
+    A = rand((M, K), 1.0, 6).cuda()
+    Bt = rand((N, K), 0.02, 7).cuda()
+    outs = []
+    for bm in (256, 128, 64):
+        C = torch.empty(M, N, dtype=torch.bfloat16, device="cuda")
+        ops.gemm(A, Bt, C, bm=bm)
+        outs.append(C)
+    torch.cuda.synchronize()
+    for c in outs[1:]:
+        assert torch.equal(outs[0], c)
+    # row slices computed alone equal the rows of the full product
+    C2 = torch.empty(128, N, dtype=torch.bfloat16, device="cuda")
+    ops.gemm(A[256:384], Bt, C2)
+    torch.cuda.synchronize()
+    assert torch.equal(C2, outs[0][256:384])
+
+
+@pytest.mark.parametrize("op", ["gelu", "silu"])
+def test_unary_ops(gpu, op):
+    announce("elementwise " + op)
+    x = rand((300, 1024), 2.0, 8)
+    y = torch.empty(300, 1024, dtype=torch.bfloat16, device="cuda")
+    ops.elementwise(op, x.cuda(), y)
+    torch.cuda.synchronize()
+    ref = O.gelu_tanh(x.float()) if op == "gelu" else O.silu(x.float())
+    close(y, ref, atol=1e-2, rtol=1e-2)
+
+
+@pytest.mark.parametrize("op", ["mul", "add", "swiglu"])
+def test_binary_ops(gpu, op):
+    announce("elementwise " + op)
+    a = rand((257, 896), 2.0, 9)
+    b = rand((257, 896), 1.0, 10)
+    y = torch.empty(257, 896, dtype=torch.bfloat16, device="cuda")
+    ops.elementwise(op, a.cuda(), y, x1=b.cuda())
+    torch.cuda.synchronize()
+    ref = {"mul": O.mul, "add": O.add, "swiglu": O.swiglu}[op](a.float(), b.float())
+    close(y, ref, atol=1e-2, rtol=1e-2)
+
+
+def test_swiglu_interleaved_matches_plain(gpu):
+    announce("swiglu_gu")
+    rows, I = 128, 1024
+    g = rand((rows, I), 2.0, 11)
+    u = rand((rows, I), 1.0, 12)
+    gu = torch.stack([g.reshape(rows, I // 8, 8), u.reshape(rows, I // 8, 8)], dim=2).reshape(rows, 2 * I)
+    y1 = torch.empty(rows, I, dtype=torch.bfloat16, device="cuda")
+    y2 = torch.empty_like(y1)
+    ops.elementwise("swiglu_gu", gu.contiguous().cuda(), y1, rows=rows, cols=I)
+    ops.elementwise("swiglu", g.cuda(), y2, x1=u.cuda())
+    torch.cuda.synchronize()
+    assert torch.equal(y1, y2)
+
+
+def test_cast_bf16_to_f16_exhaustive(gpu):
+    """All 65536 bf16 patterns; reference is numpy's fp32->fp16 (round to nearest even)."""
+    announce("cast exhaustive")
+    bits = torch.arange(65536, dtype=torch.int32).to(torch.int16)
+    x = bits.view(torch.bfloat16).reshape(512, 128)
+    y = torch.empty(512, 128, dtype=torch.float16, device="cuda")
+    ops.elementwise("cast", x.cuda(), y)
+    torch.cuda.synchronize()
+    ref = x.float().numpy().astype(np.float16)
+    got = y.cpu().numpy()
+    nan_r, nan_g = np.isnan(ref), np.isnan(got)
+    assert np.array_equal(nan_r, nan_g)
+    assert np.array_equal(ref[~nan_r].view(np.uint16), got[~nan_g].view(np.uint16))
+
+
+def test_cast_f16_to_f32(gpu):
+    announce("cast f16->f32")
+    x = rand((64, 256), 3.0, 13, torch.float16)
+    y = torch.empty(64, 256, dtype=torch.float32, device="cuda")
+    ops.elementwise("cast", x.cuda(), y)
+    torch.cuda.synchronize()
+    assert torch.equal(y.cpu(), x.float())
+
+
+@pytest.mark.parametrize("cols", [4096, 2048, 512, 128, 104])
+def test_softmax(gpu, cols):
+    announce("softmax cols=%d" % cols)
+    x = rand((333, cols), 3.0, 14)
+    y = torch.empty(333, cols, dtype=torch.bfloat16, device="cuda")
+    ops.rowop("softmax", x.cuda(), y)
+    torch.cuda.synchronize()
+    close(y, O.softmax(x.float()), atol=1e-3, rtol=1e-2)
+    s = y.float().sum(-1).cpu()
+    assert torch.all((s - 1).abs() < cols * 2 ** -8)
+
+
+@pytest.mark.parametrize("cols", [3584, 896, 4096, 128, 64])
+def test_rmsnorm_and_add_rmsnorm(gpu, cols):
+    announce("rmsnorm cols=%d" % cols)
+    a = rand((200, cols), 1.0, 15)
+    b = rand((200, cols), 1.0, 16)
+    g = (1 + rand((cols,), 0.02, 17).float()).to(torch.bfloat16)
+    y = torch.empty(200, cols, dtype=torch.bfloat16, device="cuda")
+    s = torch.empty_like(y)
+    rstd = torch.empty(200, dtype=torch.float32, device="cuda")
+    ops.rowop("add_rmsnorm", a.cuda(), y, x1=b.cuda(), gamma=g.cuda(), sum_out=s, rstd_out=rstd, eps=1e-6)
+    torch.cuda.synchronize()
+    ry, rs, rr = O.add_rmsnorm(a.float(), b.float(), g.float(), 1e-6)
+    assert torch.equal(s.cpu().float(), rs)
+    close(y, ry)
+    assert torch.allclose(rstd.cpu(), rr, rtol=1e-5)
+    y2 = torch.empty_like(y)
+    ops.rowop("rmsnorm", s, y2, gamma=g.cuda(), eps=1e-6)
+    torch.cuda.synchronize()
+    assert torch.equal(y2, y)  # fused and separate paths agree bit for bit
+
+
+def test_rope(gpu):
+    announce("rope")
+    S, Hh, D = 160, 3, 128
+    x = rand((S, Hh, D), 1.0, 18)
+    cos, sin = O.rope_tables(4096, D, 1e6)
+    xg = x.clone().cuda()
+    ops.rope(xg, S, Hh, D, cos[:S].contiguous().cuda(), sin[:S].contiguous().cuda())
+    torch.cuda.synchronize()
+    close(xg, O.rope(x.float(), cos[:S], sin[:S]), atol=1e-2, rtol=1e-2)
+
+
+def test_embedding(gpu):
+    announce("embedding")
+    table = rand((1000, 256), 0.02, 19)
+    ids = torch.randint(0, 1000, (77,), generator=torch.Generator().manual_seed(1))
+    out = torch.empty(77, 256, dtype=torch.bfloat16, device="cuda")
+    ops.embedding(table.cuda(), ids.cuda(), out)
+    torch.cuda.synchronize()
+    assert torch.equal(out.cpu(), table[ids])
+
+
+@pytest.mark.parametrize("S,HQ,HKV,D", [(128, 2, 2, 64), (256, 4, 2, 128), (200, 14, 2, 64), (384, 4, 1, 128)])
+def test_attention(gpu, S, HQ, HKV, D):
+    announce("attention S=%d HQ=%d HKV=%d D=%d" % (S, HQ, HKV, D))
+    q = rand((S, HQ, D), 1.0, 20)
+    k = rand((S, HKV, D), 1.0, 21)
+    v = rand((S, HKV, D), 1.0, 22)
+    out = torch.empty(S, HQ, D, dtype=torch.bfloat16, device="cuda")
+    ops.attention(q.cuda(), k.cuda(), v.cuda(), out, S, HQ, HKV, D)
+    torch.cuda.synchronize()
+    close(out, O.attention(q.float(), k.float(), v.float()))
+
+
+def test_attention_strided_views(gpu):
+    """q/k/v read in place from one fused [S, (HQ+2HKV)*D] buffer."""
+    announce("attention strided")
+    S, HQ, HKV, D = 256, 4, 2, 64
+    qkv = rand((S, (HQ + 2 * HKV) * D), 1.0, 23)
+    q = qkv[:, : HQ * D].reshape(S, HQ, D)
+    k = qkv[:, HQ * D:(HQ + HKV) * D].reshape(S, HKV, D)
+    v = qkv[:, (HQ + HKV) * D:].reshape(S, HKV, D)
+    g = qkv.cuda()
+    ld = (HQ + 2 * HKV) * D
+    out = torch.empty(S, HQ, D, dtype=torch.bfloat16, device="cuda")
+    ops.attention(g, g[:, HQ * D:], g[:, (HQ + HKV) * D:], out, S, HQ, HKV, D, ldq=ld, ldk=ld, ldv=ld)
+    torch.cuda.synchronize()
+    close(out, O.attention(q.float(), k.float(), v.float()))
+
+
+def test_relay_gemm_to_consumer_bit_exact(gpu):
+    """Producer GEMM releases k row tiles from its epilogue on one stream; a
+    GELU consumer on a second stream spins per tile. Output equals the unsplit
+    kernels bit for bit, every edge reports status 1, and the counters keep
+    counting across repeated runs without a host reset."""
+    announce("relay gemm->gelu k=4")
+    M, N, K, k = 1024, 1024, 512, 4
+    A = rand((M, K), 1.0, 24).cuda()
+    Bt = rand((N, K), 0.02, 25).cuda()
+    ref_c = torch.empty(M, N, dtype=torch.bfloat16, device="cuda")
+    ref_y = torch.empty_like(ref_c)
+    ops.gemm(A, Bt, ref_c)
+    ops.elementwise("gelu", ref_c, ref_y)
+    torch.cuda.synchronize()
+
+    ctrl = torch.zeros(k * ops.CTRL_WORDS, dtype=torch.int32, device="cuda")
+    C = torch.empty_like(ref_c)
+    Y = torch.empty_like(ref_c)
+    sp, sc = torch.cuda.Stream(), torch.cuda.Stream()
+    runs = 3
+    for _ in range(runs):
+        C.zero_()
+        Y.zero_()
+        torch.cuda.synchronize()
+        w = ops.make_wait(ctrl, 0, 0, M // k, adv=(0, k))
+        # consumer launched first: it must wait for the producer's releases
+        ops.elementwise("gelu", C, Y, tile_rows=M // k, grid=32, wait=w, stream=sc)
+        ops.gemm(A, Bt, C, pub=ops.make_pub(ctrl, 0, M // k), stream=sp)
+        torch.cuda.synchronize()
+        assert torch.equal(C, ref_c)
+        assert torch.equal(Y, ref_y)
+    blk = ctrl.cpu().reshape(k, ops.CTRL_WORDS)
+    assert torch.all(blk[:, 0] == runs) and torch.all(blk[:, 1] == runs)   # published == consumed
+    assert torch.all(blk[:, 2] == 1)                                        # status ok
+    assert torch.all(blk[:, 3] == 0) and torch.all(blk[:, 4] == 0)          # tickets reset
+
+
+def test_relay_wait_bound_reports_timeout(gpu):
+    """A wait on a tile nobody publishes ends at its spin bound with status 2."""
+    announce("relay timeout status")
+    ctrl = torch.zeros(2 * ops.CTRL_WORDS, dtype=torch.int32, device="cuda")
+    w = ops.make_wait(ctrl, 0, 0, 64, adv=(0, 1), max_spins=1000)
+    ops.wait(w, 0, 64)
+    torch.cuda.synchronize()
+    blk = ctrl.cpu().reshape(2, ops.CTRL_WORDS)
+    assert int(blk[0, 2]) == 2 and int(blk[0, 1]) == 1 and int(blk[0, 5]) == 0
+    # a later publish + wait succeeds and reports 1
+    ops.publish(ops.make_pub(ctrl, 0, 64), 0)
+    ops.publish(ops.make_pub(ctrl, 0, 64), 0)
+    ops.wait(w, 0, 64)
+    torch.cuda.synchronize()
+    blk = ctrl.cpu().reshape(2, ops.CTRL_WORDS)
+    assert int(blk[0, 2]) == 1 and int(blk[0, 1]) == 2 and int(blk[0, 0]) == 2

@@ -1,0 +1,149 @@
+"""kr_plan_run end to end on the GPU: DAG schedules (serial, B0, split at k)
+through the C ABI, checked against the oracle, against each other (bit-exact)
+and against the reference's recorded checksums."""
+
+import os
+
+import numpy as np
+import pytest
+import torch
+
+from kernrelay_amd import libapi, schedule, workloads
+from oracle import dag_eval
+from tests.conftest import announce
+from tests.test_oracle_dag import KATS, ref_dag
+
+pytestmark = pytest.mark.gpu
+
+
+def run(sched, tmp, name, mode="direct", env=None, iters=2, warmup=1):
+    """Run a schedule; returns (result, {node: raw 16-bit words})."""
+    path = schedule.dump_schedule(sched, tmp / (name + ".json"))
+    dump = tmp / ("dump_" + name)
+    dump.mkdir(exist_ok=True)
+    saved = {}
+    env = dict(env or {})
+    env["KR_DUMP_DIR"] = str(dump)
+    for k, v in env.items():
+        saved[k] = os.environ.get(k)
+        os.environ[k] = v
+    try:
+        announce("plan_run %s mode=%s env=%s" % (name, mode, {k: v for k, v in env.items() if k != "KR_DUMP_DIR"}))
+        r = libapi.plan_run(path, devices="0", mode=mode, iters=iters, warmup=warmup,
+                            out_json=tmp / (name + "_out.json"))
+    finally:
+        for k, v in saved.items():
+            if v is None:
+                os.environ.pop(k, None)
+            else:
+                os.environ[k] = v
+    assert r["_rc"] == 0, r
+    outs = {n["id"]: np.fromfile(dump / (n["id"] + ".bin"), dtype=np.uint16) for n in sched["nodes"]}
+    return r, outs
+
+
+def as_float(words, node):
+    odt = dag_eval.out_dtype(node)
+    if odt == "fp32":
+        return words.view(np.float32).astype(np.float64)
+    if odt == "bf16":
+        return torch.from_numpy(words.view(np.int16).copy()).view(torch.bfloat16).double().numpy()
+    return words.view(np.float16).astype(np.float64)
+
+
+def assert_close_to_oracle(sched, outs, rows=None):
+    ref = dag_eval.node_outputs(sched, rows=rows)
+    for n in sched["nodes"]:
+        r = ref[n["id"]].double().numpy().reshape(-1)
+        g = as_float(outs[n["id"]], n)[: r.size]
+        err = np.abs(g - r)
+        bound = 2e-2 + 1e-2 * np.abs(r)
+        assert np.all(err <= bound), (n["id"], float(err.max()))
+
+
+def test_tiny_mm_gelu_relay(gpu, tmp_path):
+    dag = workloads.tiny_mm_gelu(tmp_path)
+    v = workloads.variants(dag, 2)
+    base = None
+    for name, sched in v.items():
+        for mode in ("direct", "graph_per_stream"):
+            r, outs = run(sched, tmp_path, "%s_%s" % (name, mode), mode=mode)
+            assert r["ok"] and r["gate_timeouts"] == 0
+            if base is None:
+                base = outs
+                assert_close_to_oracle(sched, outs)
+            for k in outs:
+                assert np.array_equal(outs[k], base[k]), (name, mode, k)
+
+
+def test_event_sync_matches_flags(gpu, tmp_path):
+    dag = workloads.tiny_mm_gelu(tmp_path)
+    sched = schedule.build_fixed_schedule(dag, {"mm": 2, "gelu": 2})
+    _, flag = run(sched, tmp_path, "flag")
+    for mode in ("direct", "graph"):
+        _, ev = run(sched, tmp_path, "event_" + mode, mode=mode, env={"KR_SYNC": "event"})
+        for k in flag:
+            assert np.array_equal(flag[k], ev[k])
+
+
+def test_wait_kernel_variant_matches(gpu, tmp_path):
+    dag = workloads.tiny_mm_gelu(tmp_path)
+    sched = schedule.build_fixed_schedule(dag, {"mm": 2, "gelu": 2})
+    _, fused = run(sched, tmp_path, "fused")
+    _, kern = run(sched, tmp_path, "kern", env={"KR_RELAY_WAIT": "kernel"})
+    for k in fused:
+        assert np.array_equal(fused[k], kern[k])
+
+
+@pytest.mark.parametrize("chunking", [{"mm": 8, "gelu": 4}, {"mm": 2, "gelu": 8}, {"mm": 4, "gelu": 1}])
+def test_mn_row_geometry(gpu, tmp_path, chunking):
+    dag = workloads.tiny_mm_gelu(tmp_path)
+    _, base = run(schedule.serial_schedule(dag), tmp_path, "serial")
+    r, outs = run(schedule.build_fixed_schedule(dag, chunking), tmp_path, "mn")
+    assert r["ok"]
+    for k in base:
+        assert np.array_equal(base[k], outs[k]), (chunking, k)
+
+
+@pytest.mark.parametrize("name,consumers,expected", KATS[:3])
+def test_reference_checksums_on_gpu(gpu, tmp_path, name, consumers, expected):
+    """The reference's own E3/E4 DAGs (fp16, 2 ranks, DetValue inputs) split at
+    k=4 reproduce its recorded checksums within its consistency gate."""
+    dag = ref_dag(name, consumers)
+    sched = schedule.build_fixed_schedule(dag, {n.name: 4 for n in dag.nodes}, nranks=2)
+    path = schedule.dump_schedule(sched, tmp_path / "kat.json")
+    announce("plan_run KAT " + name)
+    r = libapi.plan_run(path, devices="0,0", mode="direct", iters=1, warmup=0, out_json=tmp_path / "kat_out.json")
+    assert r["_rc"] == 0 and r["ok"], r
+    assert abs(r["checksum"] - expected) / abs(expected) < 1e-3, (r["checksum"], expected)
+    assert abs(r["checksum"] - dag_eval.checksum(sched)) / abs(expected) < 1e-3
+
+
+@pytest.mark.parametrize("k", [1, 2, 4, 8])
+def test_fanout_4096_split_bit_exact(gpu, tmp_path, k):
+    """mm -> {softmax, gelu, cast} at 4096^3 bf16: every split equals serial."""
+    dag = workloads.mm_fanout(tmp_path)
+    _, base = run(schedule.serial_schedule(dag), tmp_path, "serial", iters=1, warmup=0)
+    r, outs = run(workloads.variants(dag, k)["split"], tmp_path, "split%d" % k, mode="graph_per_stream")
+    assert r["ok"] and r["gate_timeouts"] == 0
+    for node in base:
+        assert np.array_equal(base[node], outs[node]), (k, node)
+    if k == 4:
+        assert_close_to_oracle(schedule.serial_schedule(dag), outs, rows=256)
+
+
+def test_qwen_consumers_as_dag(gpu, tmp_path):
+    """The Qwen relay consumers (SwiGLU, Add+RMSNorm) behind a row-split GEMM."""
+    inputs = workloads.write_inputs(tmp_path, 512, 256, 1024)
+    raw = {"name": "mm_qwen_consumers", "nodes": [
+        {"name": "mm", "op": "matmul", "shape": {"M": 512, "K": 256, "N": 1024}, "dtype": "bf16", "inputs": inputs},
+        {"name": "swiglu", "op": "swiglu", "shape": {"rows": 512, "cols": 1024}, "dtype": "bf16"},
+        {"name": "addnorm", "op": "add_rmsnorm", "shape": {"rows": 512, "cols": 1024}, "dtype": "bf16"}],
+        "edges": [{"src": "mm", "dst": "swiglu"}, {"src": "mm", "dst": "addnorm"}]}
+    dag = schedule.dag_from_dict(raw)
+    _, base = run(schedule.serial_schedule(dag), tmp_path, "serial")
+    r, outs = run(schedule.build_fixed_schedule(dag, {"mm": 4, "swiglu": 4, "addnorm": 2}), tmp_path, "split")
+    assert r["ok"]
+    for k in base:
+        assert np.array_equal(base[k], outs[k]), k
+    assert_close_to_oracle(schedule.serial_schedule(dag), outs)

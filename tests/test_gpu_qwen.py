@@ -1,0 +1,91 @@
+"""kr_qwen_run on the GPU: every mode produces bit-identical logits (the
+relay split does not change any reduction), the last-token logits match the
+fp32 CPU oracle (|d| <= 2e-2 + 1e-2|ref|) and its argmax."""
+
+import os
+
+import numpy as np
+import pytest
+import torch
+
+from kernrelay_amd import libapi, modeldir
+from oracle import qwen as oq
+from tests.conftest import announce
+
+pytestmark = pytest.mark.gpu
+
+MODES = ["serial", "serial_fused", "serial_graph", "graph_whole", "relay_event", "relay_flag",
+         "relay_flag_graph", "relay_split:1", "relay_split:2", "relay_split:4"]
+
+
+def make(tmp, preset, seq, layers=None):
+    d = modeldir.write_model_dir(tmp / preset, preset, seq=seq, layers=layers)
+    ref = oq.write_reference(d)
+    return d, ref
+
+
+def run(d, mode, seq, dump=None, iters=2):
+    if dump:
+        os.environ["KR_DUMP_DIR"] = str(dump)
+    try:
+        announce("qwen_run %s mode=%s seq=%d" % (d.name, mode, seq))
+        r = libapi.qwen_run(d, mode=mode, seq=seq, device=0, warmup=1, iters=iters)
+    finally:
+        os.environ.pop("KR_DUMP_DIR", None)
+    assert r["_rc"] == 0, r
+    return r
+
+
+def check_logits(dump, ref):
+    w = np.fromfile(dump / "last_logits_bf16.bin", dtype=np.uint16)
+    g = torch.from_numpy(w.view(np.int16).copy()).view(torch.bfloat16).double()
+    r = ref["last_logits"].double()
+    err = (g - r).abs()
+    assert bool((err <= 2e-2 + 1e-2 * r.abs()).all()), float(err.max())
+    if ref["margin"] > 4e-2:
+        assert int(g.argmax()) == ref["argmax"]
+
+
+@pytest.mark.parametrize("preset", ["tiny-qwen2", "tiny-qwen3"])
+def test_all_modes_bit_exact_and_match_oracle(gpu, tmp_path, preset):
+    seq = 256
+    d, ref = make(tmp_path, preset, seq)
+    fnv = None
+    for mode in MODES:
+        dump = tmp_path / ("dump_" + mode.replace(":", "_"))
+        dump.mkdir()
+        r = run(d, mode, seq, dump)
+        assert r["flag_timeouts"] == 0, (mode, r)
+        assert r["ref_argmax"] == ref["argmax"]
+        check_logits(dump, ref)
+        if fnv is None:
+            fnv = r["logits_fnv64"]
+        assert r["logits_fnv64"] == fnv, (mode, r["logits_fnv64"], fnv)
+
+
+def test_qwen05_shapes_split_bit_exact(gpu, tmp_path):
+    """Qwen2.5-0.5B layer shapes (H 896, 14/2 heads, D 64, I 4864, V 151936,
+    tied) at seq 2048, two layers: serial == relay_split:4, oracle argmax."""
+    seq = 2048
+    d, ref = make(tmp_path, "qwen2.5-0.5b", seq, layers=2)
+    dump = tmp_path / "dump"
+    dump.mkdir()
+    a = run(d, "graph_whole", seq, dump)
+    check_logits(dump, ref)
+    b = run(d, "relay_split:4", seq)
+    assert a["logits_fnv64"] == b["logits_fnv64"]
+    assert b["flag_timeouts"] == 0 and b["flag_edges"] > 0
+
+
+def test_profile_many(gpu, tmp_path):
+    d = modeldir.write_model_dir(tmp_path / "tiny", "tiny-qwen2", seq=256)
+    ops = ["embedding", "rmsnorm", "add", "add_rmsnorm", "rope", "matmul_q", "matmul_k", "matmul_v",
+           "attention", "matmul_o", "matmul_gate", "matmul_up", "silu", "mul", "swiglu", "matmul_down",
+           "matmul_lm"]
+    cases = [{"op": op, "k": k} for op in ops for k in (1, 2, 4)]
+    announce("profile_many tiny")
+    r = libapi.qwen_profile_many(d, cases, seq=256, device=0)
+    assert r["_rc"] == 0, r
+    got = {(c["op"], c["k"]) for c in r["cases"] if "best_us" in c}
+    assert got == {(c["op"], c["k"]) for c in cases}
+    assert all(c["best_us"] > 0 for c in r["cases"])
