@@ -1,0 +1,188 @@
+"""Headline benchmark: Qwen2.5-7B-shaped bf16 prefill at seq 2048 on one
+MI355X through kr_qwen_run — serial (graph_whole) vs relay split at 4 tiles —
+plus the producer GEMM's roofline and the CPU (oracle) baseline.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--tiles 4] [--preset qwen2.5-7b]
+
+Prints ONE JSON line. A step is one full prefill (28 layers + lm_head over all
+2048 rows) with weights and inputs resident in HBM; `value` is tokens/s of the
+relay-split prefill over exactly K timed steps (each step bracketed by device
+synchronisation inside the library). Weights are random-init N(0, 0.02)
+(`data: synthetic`): no checkpoint can be fetched on this pool.
+"""
+
+import argparse
+import json
+import os
+import shutil
+import sys
+import tempfile
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+PEAK_BF16_TFLOPS = 2500.0     # MI355X dense bf16 MFMA peak (vendor figure, no sparsity)
+PEAK_HBM_GBS = 8000.0
+REF_BEST_TOK_S = 2048 / 0.1462  # reference graph_whole, Qwen2.5-7B seq 2048, Ascend 910B3 (RESULTS.md:21)
+
+
+def log(msg):
+    print("[bench] " + msg, file=sys.stderr, flush=True)
+
+
+def gemm_roofline(M, N, K, reps=20):
+    """Average duration of the producer GEMM at the dominant prefill shape,
+    timed with HIP events on the stream it is launched on."""
+    import torch
+
+    from kernrelay_amd import ops
+
+    g = torch.Generator(device="cuda").manual_seed(7)
+    A = torch.randn(M, K, device="cuda", generator=g).to(torch.bfloat16)
+    Bt = (torch.randn(N, K, device="cuda", generator=g) * 0.02).to(torch.bfloat16)
+    C = torch.empty(M, N, device="cuda", dtype=torch.bfloat16)
+    s = torch.cuda.current_stream()
+    for _ in range(3):
+        ops.gemm(A, Bt, C, stream=s)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(s)
+    for _ in range(reps):
+        ops.gemm(A, Bt, C, stream=s)
+    e1.record(s)
+    torch.cuda.synchronize()
+    avg_s = e0.elapsed_time(e1) / 1e3 / reps
+    flops = 2.0 * M * N * K
+    achieved = flops / avg_s / 1e12
+    del A, Bt, C
+    torch.cuda.empty_cache()
+    return {"bound": "mfma", "achieved": round(achieved, 1), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+            "frac": round(achieved / PEAK_BF16_TFLOPS, 4), "traffic": None,
+            "kernel": "GemmKernel (gate/up projection) %dx%dx%d bf16" % (M, N, K),
+            "avg_launch_us": round(avg_s * 1e6, 2), "launches": reps}
+
+
+def cpu_baseline(model_dir, seconds_hint=20):
+    """Oracle (fp32 torch CPU) on a bounded sample: decoder layer 0 and the
+    lm_head over all rows at seq 2048; scaled to the full prefill as
+    L * t_layer + t_lm_head."""
+    import torch
+
+    from oracle import ops as O
+    from oracle import qwen as oq
+
+    # the CPU share this process may use (affinity), at most 16 on the GPU box
+    threads = max(1, min(16, len(os.sched_getaffinity(0))))
+    torch.set_num_threads(threads)
+    m = oq.ModelDir(model_dir)
+    ids = m.ids()
+    S = ids.numel()
+    cos, sin = m.rope(S)
+    with torch.no_grad():
+        h = O.embedding(m.tensor("embed.weight"), ids)
+        x, _ = O.rmsnorm(h, m.tensor("L00.input_layernorm.weight"), m.eps)
+        t0 = time.perf_counter()
+        h2, d = oq.layer_forward(m, 0, h, x, cos, sin)
+        x, h, _ = O.add_rmsnorm(h2, d, m.tensor("L01.input_layernorm.weight"), m.eps)
+        t_layer = time.perf_counter() - t0
+        w = m.tensor("lm_head.weight_t")
+        t0 = time.perf_counter()
+        O.gemm(x, w)
+        t_lm = time.perf_counter() - t0
+    total = m.L * t_layer + t_lm
+    return {"value": round(S / total, 2), "unit": "tok/s", "cores": threads, "kind": "port",
+            "sample": "oracle fp32 torch-CPU: decoder layer 0 (%.2f s) + lm_head over %d rows (%.2f s) "
+                      "at seq %d, scaled to %d layers" % (t_layer, S, t_lm, S, m.L),
+            "ms_per_prefill_est": round(total * 1e3, 1)}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=2)
+    ap.add_argument("--tiles", type=int, default=4)
+    ap.add_argument("--seq", type=int, default=2048)
+    ap.add_argument("--preset", default="qwen2.5-7b")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--keep", default=None, help="keep / reuse the model directory here")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print("bench.py: this build targets one GPU; --gpus %d is not supported (the relay path is "
+              "single-device; see DESIGN.md for how it would shard)" % args.gpus, file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    from kernrelay_amd import libapi, modeldir
+
+    libapi.lib()
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        sys.exit(1)
+    cfg = dict(modeldir.PRESETS[args.preset])
+    S = args.seq
+    base = "/dev/shm" if os.path.isdir("/dev/shm") and shutil.disk_usage("/dev/shm").free > 40e9 else None
+    tmp = Path(args.keep) if args.keep else Path(tempfile.mkdtemp(prefix="kr_bench_", dir=base))
+    try:
+        if not (tmp / "manifest.json").exists():
+            t0 = time.time()
+            log("writing %s model dir (seq %d) to %s" % (args.preset, S, tmp))
+            modeldir.write_model_dir(tmp, args.preset, seq=S, device="cuda")
+            torch.cuda.synchronize()
+            torch.cuda.empty_cache()
+            log("model dir written in %.1f s" % (time.time() - t0))
+        runs = {}
+        for mode in ("graph_whole", "relay_split:%d" % args.tiles):
+            log("kr_qwen_run %s (warmup %d, steps %d)" % (mode, args.warmup, args.steps))
+            r = libapi.qwen_run(tmp, mode=mode, seq=S, device=0, warmup=args.warmup, iters=args.steps)
+            if r.get("_rc") != 0:
+                raise RuntimeError("%s failed: %s" % (mode, r.get("error")))
+            log("  best %.1f us typical %.1f us argmax %s timeouts %s" % (
+                r["best_us"], r["typical_us"], r["argmax"], r["flag_timeouts"]))
+            runs[mode] = r
+        serial, split = runs["graph_whole"], runs["relay_split:%d" % args.tiles]
+        if serial["logits_fnv64"] != split["logits_fnv64"]:
+            raise RuntimeError("relay split logits differ from serial")
+        I, H = cfg["intermediate_size"], cfg["hidden_size"]
+        log("gemm roofline %dx%dx%d" % (S, 2 * I, H))
+        roof = gemm_roofline(S, 2 * I, H)
+        total_split_s = sum(split["samples_us"]) / 1e6
+        total_serial_s = sum(serial["samples_us"]) / 1e6
+        value = args.steps * S / total_split_s
+        flops = modeldir.model_flops(cfg, S)
+        cpu = None
+        if not args.no_cpu:
+            log("cpu baseline (oracle, bounded sample)")
+            cpu = cpu_baseline(tmp)
+        out = {
+            "metric": "Qwen2.5-7B prefill tok/s @seq2048 1 GPU; split-vs-serial speedup; MFMA util",
+            "value": round(value, 1), "unit": "tok/s", "n_gpus": 1, "steps": args.steps,
+            "warmup": args.warmup, "ms_per_step": round(total_split_s * 1e3 / args.steps, 3),
+            "higher_is_better": True, "scaling": "weak",
+            "vs_baseline": round(value / REF_BEST_TOK_S, 3), "dtype": "bf16",
+            "data": "synthetic (random-init N(0,0.02) bf16 weights, uniform token ids)",
+            "config": {"workload": "Qwen2.5-7B-shaped prefill, batch 1, seq %d, relay split %d tiles"
+                       % (S, args.tiles), "model": args.preset, "global_batch": 1, "seq_len": S,
+                       "parallelism": "none (1 GPU)", "tiles": args.tiles},
+            "serial_ms_per_step": round(total_serial_s * 1e3 / args.steps, 3),
+            "serial_tok_s": round(args.steps * S / total_serial_s, 1),
+            "split_vs_serial": round(total_serial_s / total_split_s, 4),
+            "best_ms": {"serial": round(serial["best_us"] / 1e3, 3), "split": round(split["best_us"] / 1e3, 3)},
+            "prefill_tflops": round(flops / 1e12, 3),
+            "prefill_mfma_frac": round(flops / (total_split_s / args.steps) / 1e12 / PEAK_BF16_TFLOPS, 4),
+            "roofline": roof,
+            "cpu_baseline": cpu,
+            "bit_exact_serial_vs_split": True,
+            "argmax": split["argmax"], "flag_edges": split["flag_edges"], "flag_timeouts": split["flag_timeouts"],
+        }
+        print(json.dumps(out), flush=True)
+    finally:
+        if not args.keep:
+            shutil.rmtree(tmp, ignore_errors=True)
+
+
+if __name__ == "__main__":
+    main()

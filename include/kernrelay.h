@@ -62,7 +62,7 @@ int kr_qwen_run(const char *model_dir, const char *mode, int seq, int device,
 /*
  * Two-GPU pipeline-parallel prefill. Not built on this single-GPU target:
  * always returns 1 with {"error":"multi-GPU not in scope"}.
- * Replaces reference exec/qwen_main.cpp:2258-2285.
+ * Replaces reference exec/qwen_main.cpp:2256-2285.
  */
 int kr_qwen_pp_run(const char *model_dir, const char *mode, int seq, int dev0,
                    int dev1, int requests, int warmup, int iters, char *out,
@@ -71,7 +71,7 @@ int kr_qwen_pp_run(const char *model_dir, const char *mode, int seq, int dev0,
 /*
  * Two-GPU tensor-parallel MLP prefill. Not built on this single-GPU target:
  * always returns 1 with {"error":"multi-GPU not in scope"}.
- * Replaces reference exec/qwen_main.cpp:2229-2256.
+ * Replaces reference exec/qwen_main.cpp:2225-2254.
  */
 int kr_qwen_tp_run(const char *model_dir, const char *mode, int seq, int dev0,
                    int dev1, int tiles, int warmup, int iters, char *out,
@@ -84,7 +84,7 @@ int kr_qwen_tp_run(const char *model_dir, const char *mode, int seq, int dev0,
  * exec/qwen_main.cpp:1535-1783). Ops: matmul_q/k/v/o/gate/up/down/lm, add,
  * rmsnorm, add_rmsnorm, rope, silu, mul, swiglu, embedding, attention.
  * Returns 0 on success; 1 with {"error":...} in `out` on failure.
- * Replaces reference exec/qwen_main.cpp:2201-2227.
+ * Replaces reference exec/qwen_main.cpp:2198-2223.
  */
 int kr_qwen_profile_many(const char *model_dir, const char *spec_json, int seq,
                          int device, char *out, size_t out_cap);

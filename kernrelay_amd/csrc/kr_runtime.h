@@ -109,28 +109,37 @@ inline std::vector<uint32_t> ConsumerCuMask(int num_cus, int per_xcd)
     return mask;
 }
 
-// Producer + consumer stream pair. The consumer stream is optionally
-// CU-masked (KR_CONSUMER_CUS_PER_XCD = 1..4) so spinning consumers can only
-// ever occupy those CUs; the producer keeps the whole device.
+// Producer + consumer stream pair, each on its own hardware queue.
+//
+// The relay waits in both directions on the device (consumer kernels spin on
+// producer tiles, the producer's one-workgroup waits spin on consumer
+// releases), so the two streams must run concurrently. Ordinary streams are
+// multiplexed onto a few hardware queues once a process holds more streams
+// than GPU_MAX_HW_QUEUES (a torch stream pool alone creates 32): two streams on
+// one queue would run a captured producer graph to completion before the
+// consumer graph starts. A CU-masked stream always gets a queue of its own, so
+// both streams are created with explicit CU masks: the producer with every
+// CU, the consumer with every CU or, with KR_CONSUMER_CUS_PER_XCD = 1..4, a
+// few CUs per XCD so spinning consumers can only ever occupy those.
 struct StreamPair {
     hipStream_t prod = nullptr;
     hipStream_t cons = nullptr;
-    int cons_cus = 0;  // 0 = unmasked
+    int cons_cus = 0;  // CUs in the consumer mask
+    int prod_cus = 0;
 
     void Create(int device)
     {
-        Check(hipStreamCreateWithFlags(&prod, hipStreamNonBlocking), "create producer stream");
+        hipDeviceProp_t prop;
+        Check(hipGetDeviceProperties(&prop, device), "device props");
+        const int ncu = prop.multiProcessorCount;
+        std::vector<uint32_t> all((ncu + 31) / 32, 0u);
+        for (int c = 0; c < ncu; ++c) all[c / 32] |= 1u << (c % 32);
+        Check(hipExtStreamCreateWithCUMask(&prod, uint32_t(all.size()), all.data()), "create producer stream");
+        prod_cus = ncu;
         const int per_xcd = EnvInt("KR_CONSUMER_CUS_PER_XCD", 0);
-        if (per_xcd > 0) {
-            hipDeviceProp_t prop;
-            Check(hipGetDeviceProperties(&prop, device), "device props");
-            auto mask = ConsumerCuMask(prop.multiProcessorCount, per_xcd);
-            Check(hipExtStreamCreateWithCUMask(&cons, uint32_t(mask.size()), mask.data()),
-                  "create CU-masked consumer stream");
-            for (uint32_t w : mask) cons_cus += __builtin_popcount(w);
-        } else {
-            Check(hipStreamCreateWithFlags(&cons, hipStreamNonBlocking), "create consumer stream");
-        }
+        std::vector<uint32_t> mask = per_xcd > 0 ? ConsumerCuMask(ncu, per_xcd) : all;
+        Check(hipExtStreamCreateWithCUMask(&cons, uint32_t(mask.size()), mask.data()), "create consumer stream");
+        for (uint32_t w : mask) cons_cus += __builtin_popcount(w);
     }
     void Destroy()
     {
