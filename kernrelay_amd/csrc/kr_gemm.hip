@@ -46,6 +46,35 @@ struct GemmParams {
 
 __device__ __forceinline__ int Swz(int row, int chunk) { return chunk ^ ((row >> 1) & 7); }
 
+// Workgroup -> output tile. The dispatcher deals workgroups to the 8 XCDs
+// round-robin (XCD = blockIdx % 8) and each XCD has its own L2.
+// * No relay: XCD x takes a contiguous run of tile ids and walks it
+//   column-major (row blocks fastest), so a weight column block is read by
+//   consecutive workgroups of one XCD while it sits in that XCD's L2.
+// * Relay: relay tiles are dispatched front to back (each must complete as
+//   early as possible); inside a relay tile the order is column-major so its
+//   row blocks share each weight block.
+__device__ __forceinline__ void TileOf(int bid, int tiles_m, int tiles_n, int bm, const RelayPub &pub, int &tm,
+                                       int &tn)
+{
+    if (pub.ctrl != nullptr) {
+        const int mt = pub.rows_per_tile / bm;  // row blocks per relay tile
+        const int per = mt * tiles_n;
+        const int r = bid / per;
+        const int local = bid - r * per;
+        tm = r * mt + local % mt;
+        tn = local / mt;
+        return;
+    }
+    const int T = tiles_m * tiles_n;
+    const int xcd = bid & 7;
+    const int slot = bid >> 3;
+    const int q = T >> 3, rem = T & 7;
+    const int t = xcd < rem ? xcd * (q + 1) + slot : rem * (q + 1) + (xcd - rem) * q + slot;
+    tm = t % tiles_m;
+    tn = t / tiles_m;
+}
+
 template <int DT>
 __device__ __forceinline__ f32x16 Mfma(const uint4 &a, const uint4 &b, const f32x16 &c)
 {
@@ -77,11 +106,8 @@ GemmKernel(GemmParams p)
     const int wm = wave >> 1;
     const int wn = wave & 1;
 
-    // Row-tile-major order: all column blocks of a row block are dispatched
-    // together, so relay tiles complete front to back.
-    const int bid = blockIdx.x;
-    const int tm = bid / p.tiles_n;
-    const int tn = bid % p.tiles_n;
+    int tm, tn;
+    TileOf(blockIdx.x, p.tiles_m, p.tiles_n, BM, p.pub, tm, tn);
     const int m0 = tm * BM;
     const int n0 = tn * BN;
 
@@ -204,6 +230,20 @@ GemmKernel(GemmParams p)
     if (p.pub.ctrl != nullptr) RelayArrive(p.pub, m0 / p.pub.rows_per_tile);
 }
 
+// ---------------------------------------------------------------------------
+#include "kr_gemm_pipe.inc"
+
+// KR_GEMM_SIMPLE=1 routes every shape through GemmKernel (A/B comparison of
+// the two main loops; both give identical bits).
+bool ForceSimple()
+{
+    static const bool v = [] {
+        const char *e = std::getenv("KR_GEMM_SIMPLE");
+        return e != nullptr && *e == '1';
+    }();
+    return v;
+}
+
 template <int DT, int BM, int BN>
 void LaunchTyped(const GemmParams &base, hipStream_t stream)
 {
@@ -215,7 +255,11 @@ void LaunchTyped(const GemmParams &base, hipStream_t stream)
         p.pub.arrivals = (p.pub.rows_per_tile / BM) * p.tiles_n;
     }
     const dim3 grid(p.tiles_m * p.tiles_n);
-    hipLaunchKernelGGL((GemmKernel<DT, BM, BN>), grid, dim3(kThreads), 0, stream, p);
+    if (p.K % kStageK == 0 && !ForceSimple()) {
+        hipLaunchKernelGGL((GemmPipeKernel<DT, BM, BN>), grid, dim3(kThreads), 0, stream, p);
+    } else {
+        hipLaunchKernelGGL((GemmKernel<DT, BM, BN>), grid, dim3(kThreads), 0, stream, p);
+    }
     Check(hipGetLastError(), "gemm launch");
 }
 
@@ -274,6 +318,11 @@ void GemmLaunch(const GemmDesc &d, hipStream_t stream)
     p.pub = d.pub;
     const int relay_rows = d.pub.ctrl != nullptr ? d.pub.rows_per_tile : 0;
     GemmTile t = GemmPickTile(d.M, d.N, relay_rows);
+    if (const char *e = std::getenv("KR_GEMM_TILE")) {
+        // tile sweep override "BMxBN" (measurement aid; bits are unchanged)
+        int bm = 0, bn = 0;
+        if (std::sscanf(e, "%dx%d", &bm, &bn) == 2 && (relay_rows == 0 || relay_rows % bm == 0)) t = {bm, bn};
+    }
     if (d.bm > 0) {
         // a forced M tile pairs with the widest N tile built for it
         t.bm = d.bm;
