@@ -14,10 +14,14 @@
 // * Every variant uses the same MFMA instruction and the same K order, so a
 //   row of C is bit-identical whatever BM/BN or row range a launch covers:
 //   the split schedule is bit-exact against the unsplit one.
+// * The MFMA is fed (B fragment, A fragment), so each 32x32 accumulator block
+//   holds C^T: every lane owns four runs of 4 consecutive columns of one row.
 // * Epilogue: acc -> 16-bit (RNE); with bias, bf16(bf16(acc)+bias) — the
 //   rounding of the reference's separate Matmul then Add (EmitQkv,
-//   exec/qwen_main.cpp:1336-1344). Then the workgroup arrives on its row
-//   tile's relay counter; the last arrival releases the tile.
+//   exec/qwen_main.cpp:1336-1344). The tile is staged row-major in LDS
+//   (8-byte writes, XOR-swizzled) and leaves as full-line 16-byte stores. Then
+//   the workgroup arrives on its row tile's relay counter; the last arrival
+//   releases the tile.
 #include "kr_gemm.h"
 #include "kr_relay.h"
 
@@ -84,6 +88,71 @@ __device__ __forceinline__ f32x16 Mfma(const uint4 &a, const uint4 &b, const f32
     } else {
         return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a),
                                                       __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+    }
+}
+
+// Write the workgroup's BMxBN tile of C. acc[i][j] is the C^T block of rows
+// wm*BM/2 + 32i.., cols wn*BN/2 + 32j..: value v of lane l sits at row l%32,
+// col 8*(v/4) + 4*(l/32) + v%4. Each run of 4 columns goes to LDS as one
+// 8-byte write into a row-major tile whose 8-byte slots are XOR-swizzled with
+// row & 31 (32 rows of one column run hit 32 distinct bank pairs); then every
+// thread copies 16-byte row chunks to C (8 lanes cover a 128-byte line).
+// `stage` must hold BM*BN 16-bit values and be free (all waves past their
+// last LDS read of the main loop).
+template <int DT, int BM, int BN, int MI, int NI>
+__device__ __forceinline__ void StoreTile(const GemmParams &p, f32x16 (&acc)[MI][NI], uint16_t *stage, int m0,
+                                          int n0, int wm, int wn, int lane)
+{
+    static_assert(BN >= 128, "slot swizzle needs >= 32 slots per row");
+    const int lrow = lane & 31;
+    const int lhalf = lane >> 5;
+#pragma unroll
+    for (int j = 0; j < NI; ++j) {
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            const int col = wn * (BN / 2) + j * 32 + 8 * g + 4 * lhalf;
+            float b[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+            if (p.bias != nullptr) {
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    if (n0 + col + e < p.N) b[e] = Elem<DT>::Load(p.bias[n0 + col + e]);
+            }
+#pragma unroll
+            for (int i = 0; i < MI; ++i) {
+                const int row = wm * (BM / 2) + i * 32 + lrow;
+                uint32_t h[4];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const float x = acc[i][j][4 * g + e];
+                    h[e] = p.bias != nullptr ? Elem<DT>::Store(RoundTo<DT>(x) + b[e]) : Elem<DT>::Store(x);
+                }
+                const int slot = (col >> 2) ^ (row & 31);
+                *reinterpret_cast<uint2 *>(stage + row * BN + slot * 4) =
+                    make_uint2(h[0] | (h[1] << 16), h[2] | (h[3] << 16));
+            }
+        }
+    }
+    __syncthreads();
+    constexpr int CPR = BN / 8;  // 16-byte chunks per row
+    const bool vec = (p.ldc % 8 == 0) && ((reinterpret_cast<uintptr_t>(p.C) & 15) == 0);
+#pragma unroll 4
+    for (int idx = threadIdx.x; idx < BM * CPR; idx += kThreads) {
+        const int row = idx / CPR;
+        const int ch = idx % CPR;
+        const int gm = m0 + row;
+        const int gn = n0 + ch * 8;
+        if (gm >= p.M || gn >= p.N) continue;
+        uint4 v = *reinterpret_cast<const uint4 *>(stage + row * BN + (ch ^ ((row & 31) >> 1)) * 8);
+        if (row & 1) v = make_uint4(v.z, v.w, v.x, v.y);
+        uint16_t *dst = p.C + int64_t(gm) * p.ldc + gn;
+        if (vec && gn + 8 <= p.N) {
+            *reinterpret_cast<uint4 *>(dst) = v;
+        } else {
+            const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+            for (int e = 0; e < 8; ++e)
+                if (gn + e < p.N) dst[e] = uint16_t(w[e >> 1] >> ((e & 1) * 16));
+        }
     }
 }
 
@@ -194,39 +263,13 @@ GemmKernel(GemmParams p)
 #pragma unroll
             for (int i = 0; i < MI; ++i)
 #pragma unroll
-                for (int j = 0; j < NI; ++j) acc[i][j] = Mfma<DT>(fa[i], fb[j], acc[i][j]);
+                for (int j = 0; j < NI; ++j) acc[i][j] = Mfma<DT>(fb[j], fa[i], acc[i][j]);
         }
         if (kt + 1 < nk) store_lds(cur ^ 1);
         __syncthreads();
     }
 
-    // Epilogue. 32x32 accumulator layout: value v of lane l is
-    // row 8*(v/4) + 4*(l/32) + v%4, column l%32 of the block.
-#pragma unroll
-    for (int j = 0; j < NI; ++j) {
-        const int col = n0 + wn * (BN / 2) + j * 32 + frow;
-        if (col >= p.N) continue;
-        float bcol = 0.0f;
-        if (p.bias != nullptr) bcol = Elem<DT>::Load(p.bias[col]);
-#pragma unroll
-        for (int i = 0; i < MI; ++i) {
-#pragma unroll
-            for (int v = 0; v < 16; ++v) {
-                const int row = m0 + wm * (BM / 2) + i * 32 + 8 * (v >> 2) + 4 * fhalf + (v & 3);
-                if (row < p.M) {
-                    float x = acc[i][j][v];
-                    uint16_t o;
-                    if (p.bias != nullptr) {
-                        o = Elem<DT>::Store(RoundTo<DT>(x) + bcol);
-                    } else {
-                        o = Elem<DT>::Store(x);
-                    }
-                    p.C[int64_t(row) * p.ldc + col] = o;
-                }
-            }
-        }
-    }
-
+    StoreTile<DT, BM, BN>(p, acc, smem, m0, n0, wm, wn, lane);
     if (p.pub.ctrl != nullptr) RelayArrive(p.pub, m0 / p.pub.rows_per_tile);
 }
 
@@ -244,6 +287,17 @@ bool ForceSimple()
     return v;
 }
 
+// L2 prefetch distance of the pipelined kernel in K stages (KR_GEMM_PF: 0
+// default = off, 2, 4); it changes timing only, never the bits.
+int PrefetchStages()
+{
+    static const int v = [] {
+        const char *e = std::getenv("KR_GEMM_PF");
+        return e != nullptr ? std::atoi(e) : 0;
+    }();
+    return v;
+}
+
 template <int DT, int BM, int BN>
 void LaunchTyped(const GemmParams &base, hipStream_t stream)
 {
@@ -255,8 +309,12 @@ void LaunchTyped(const GemmParams &base, hipStream_t stream)
         p.pub.arrivals = (p.pub.rows_per_tile / BM) * p.tiles_n;
     }
     const dim3 grid(p.tiles_m * p.tiles_n);
-    if (p.K % kStageK == 0 && !ForceSimple()) {
-        hipLaunchKernelGGL((GemmPipeKernel<DT, BM, BN>), grid, dim3(kThreads), 0, stream, p);
+    if (p.K % kPipeK == 0 && !ForceSimple()) {
+        switch (PrefetchStages()) {
+        case 2: hipLaunchKernelGGL((GemmPipeKernel<DT, BM, BN, 2>), grid, dim3(kThreads), 0, stream, p); break;
+        case 4: hipLaunchKernelGGL((GemmPipeKernel<DT, BM, BN, 4>), grid, dim3(kThreads), 0, stream, p); break;
+        default: hipLaunchKernelGGL((GemmPipeKernel<DT, BM, BN, 0>), grid, dim3(kThreads), 0, stream, p); break;
+        }
     } else {
         hipLaunchKernelGGL((GemmKernel<DT, BM, BN>), grid, dim3(kThreads), 0, stream, p);
     }
