@@ -5,7 +5,9 @@
 // the upper-triangular mask of MakeMask :487-497).
 //
 // One workgroup = 128 queries of one head (4 waves x 32 queries); keys and
-// values stream through LDS in blocks of 64. The kernel computes the
+// values stream through a double-buffered LDS ring in blocks of 64: block
+// kb+1 is loaded into registers while block kb is computed, then written to
+// the other buffer, one barrier per block. The kernel computes the
 // transposed products so that every operand lands where the next MFMA wants
 // it, with no cross-lane shuffles of P:
 //   S^T = K . Q^T   (32x32x16: A = K rows from LDS, B = Q rows in registers)
@@ -14,9 +16,12 @@
 //   O^T += V^T . P^T (A = V^T from a transposed LDS copy, B = P^T straight
 //          from the S^T accumulators after rounding to 16 bits).
 // MFMA pairs A slot s with B slot s, so the key order inside a 16-key step
-// only has to agree between V^T and P^T; it is the accumulator's own row
-// order {4h..4h+3, 8+4h..8+4h+3}.
+// only has to agree between V^T and P^T. P^T's order is the accumulator's
+// {4h..4h+3, 8+4h..8+4h+3} for lane half h; V^T rows are stored with the keys
+// of each 16-key group permuted into exactly that order, so one ds_read_b128
+// fetches a lane's 8 keys.
 // Online softmax in base 2 (scores pre-scaled by scale*log2(e)), fp32 state.
+// Workgroups run heaviest (longest causal rows) first across all heads.
 #include "kr_misc.h"
 
 namespace kr {
@@ -59,24 +64,28 @@ __device__ __forceinline__ int KSwz(int r, int c)
     else return c ^ ((r >> 1) & 7);
 }
 
-// 8-byte unit u (4 keys) of row d of V^T.
-__device__ __forceinline__ int VSwz(int d, int u) { return u ^ (d & 15); }
+// V^T rows hold 64 keys = 8 chunks of 16 bytes; chunk c of row d sits in
+// slot c ^ VSwz(d) (distinct slots for 8- and 16-lane passes).
+__device__ __forceinline__ int VSwz(int d) { return (d & 7) ^ ((d >> 3) & 1); }
 
 template <int DT, int D>
-__global__ void __launch_bounds__(256) AttnKernel(AttnParams p)
+__global__ void __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_waves_per_eu(2))) AttnKernel(AttnParams p)
 {
-    constexpr int DCH = D / 8;
+    constexpr int DCH = D / 8;                       // 16-byte chunks per K/V row
     constexpr int DBLK = D / 32;
-    __shared__ __attribute__((aligned(16))) uint16_t Ks[kKvBlk * D];
-    __shared__ __attribute__((aligned(16))) uint16_t Vt[D * kKvBlk];
+    constexpr int KL = kKvBlk * DCH / 256;           // K chunks per thread per block
+    constexpr int VG = (kKvBlk / 4) * DCH;           // V (4 keys x 8 d) groups per block
+    constexpr int VL = (VG + 255) / 256;             // V groups per thread
+    __shared__ __attribute__((aligned(16))) uint16_t Ks[2][kKvBlk * D];
+    __shared__ __attribute__((aligned(16))) uint16_t Vt[2][D * kKvBlk];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
     const int hf = lane >> 5;
-    const int h = blockIdx.y;
     const int nqb = (p.S + kQBlk - 1) / kQBlk;
-    const int qb = nqb - 1 - int(blockIdx.x);  // longest causal rows first
+    const int h = int(blockIdx.x) % p.HQ;
+    const int qb = nqb - 1 - int(blockIdx.x) / p.HQ;  // longest causal rows first, all heads
     const int q0 = qb * kQBlk;
     const int kvh = h / (p.HQ / p.HKV);
     const int64_t ldq = p.ldq;
@@ -104,104 +113,143 @@ __global__ void __launch_bounds__(256) AttnKernel(AttnParams p)
     const int q_hi = min(q0 + kQBlk - 1, p.S - 1);
     const int nkb = q_hi / kKvBlk + 1;
 
-    for (int kb = 0; kb < nkb; ++kb) {
+    // block kb -> registers (rows past S read as zero)
+    uint4 kr[KL];
+    uint4 vr[VL][4];
+    auto load = [&](int kb) {
         const int kv0 = kb * kKvBlk;
-        __syncthreads();
-        for (int t = tid; t < kKvBlk * DCH; t += 256) {
-            const int r = t / DCH, c = t % DCH;
-            const int kv = kv0 + r;
-            uint4 val = make_uint4(0, 0, 0, 0);
-            if (kv < p.S) val = *reinterpret_cast<const uint4 *>(p.k + int64_t(kv) * p.ldk + int64_t(kvh) * D + c * 8);
-            *reinterpret_cast<uint4 *>(Ks + r * D + KSwz<D>(r, c) * 8) = val;
+#pragma unroll
+        for (int i = 0; i < KL; ++i) {
+            const int t = tid + 256 * i;
+            const int kv = kv0 + t / DCH;
+            kr[i] = kv < p.S ? *reinterpret_cast<const uint4 *>(p.k + int64_t(kv) * p.ldk + int64_t(kvh) * D + (t % DCH) * 8)
+                             : make_uint4(0, 0, 0, 0);
         }
-        for (int t = tid; t < (kKvBlk / 4) * DCH; t += 256) {
-            const int g = t / DCH, c = t % DCH;
-            U16x8 rows[4];
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int kv = kv0 + 4 * g + i;
-                if (kv < p.S) {
-                    rows[i] = LoadU16x8(p.v + int64_t(kv) * p.ldv + int64_t(kvh) * D + c * 8);
-                } else {
+        for (int i = 0; i < VL; ++i) {
+            const int t = tid + 256 * i;
+            const int grp = t / DCH, c = t % DCH;
 #pragma unroll
-                    for (int e = 0; e < 8; ++e) rows[i].v[e] = 0;
-                }
+            for (int r = 0; r < 4; ++r) {
+                const int kv = kv0 + 4 * grp + r;
+                vr[i][r] = (t < VG && kv < p.S)
+                               ? *reinterpret_cast<const uint4 *>(p.v + int64_t(kv) * p.ldv + int64_t(kvh) * D + c * 8)
+                               : make_uint4(0, 0, 0, 0);
             }
+        }
+    };
+    // registers -> LDS buffer b: K row-major (swizzled), V transposed with
+    // each 16-key group permuted to the P^T slot order
+    auto store = [&](int b) {
+#pragma unroll
+        for (int i = 0; i < KL; ++i) {
+            const int t = tid + 256 * i;
+            const int r = t / DCH, c = t % DCH;
+            *reinterpret_cast<uint4 *>(&Ks[b][r * D + KSwz<D>(r, c) * 8]) = kr[i];
+        }
+#pragma unroll
+        for (int i = 0; i < VL; ++i) {
+            const int t = tid + 256 * i;
+            if (t >= VG) continue;
+            const int ap = t / DCH, c = t % DCH;  // keys 4ap..4ap+3, d chunk c
+            const int u = 4 * (ap >> 2) + ((ap & 3) >> 1) + 2 * (ap & 1);  // 8-byte unit in the row
+            const uint32_t w0[4] = {vr[i][0].x, vr[i][0].y, vr[i][0].z, vr[i][0].w};
+            const uint32_t w1[4] = {vr[i][1].x, vr[i][1].y, vr[i][1].z, vr[i][1].w};
+            const uint32_t w2[4] = {vr[i][2].x, vr[i][2].y, vr[i][2].z, vr[i][2].w};
+            const uint32_t w3[4] = {vr[i][3].x, vr[i][3].y, vr[i][3].z, vr[i][3].w};
 #pragma unroll
             for (int e = 0; e < 8; ++e) {
                 const int d = c * 8 + e;
-                uint2 w;
-                w.x = uint32_t(rows[0].v[e]) | (uint32_t(rows[1].v[e]) << 16);
-                w.y = uint32_t(rows[2].v[e]) | (uint32_t(rows[3].v[e]) << 16);
-                *reinterpret_cast<uint2 *>(Vt + d * kKvBlk + VSwz(d, g) * 4) = w;
+                const int sh = (e & 1) * 16;
+                const uint32_t k0 = (w0[e >> 1] >> sh) & 0xffffu, k1 = (w1[e >> 1] >> sh) & 0xffffu;
+                const uint32_t k2 = (w2[e >> 1] >> sh) & 0xffffu, k3 = (w3[e >> 1] >> sh) & 0xffffu;
+                *reinterpret_cast<uint2 *>(&Vt[b][d * kKvBlk + (((u >> 1) ^ VSwz(d)) * 8) + (u & 1) * 4]) =
+                    make_uint2(k0 | (k1 << 16), k2 | (k3 << 16));
             }
         }
+    };
+
+    load(0);
+    store(0);
+    __syncthreads();
+
+    for (int kb = 0; kb < nkb; ++kb) {
+        const int kv0 = kb * kKvBlk;
+        const int cur = kb & 1;
+        const bool more = kb + 1 < nkb;
+        if (more) load(kb + 1);
+
+        if (kv0 <= wave_q_hi) {  // else: block entirely in this wave's future
+            const uint16_t *K = Ks[cur];
+            const uint16_t *V = Vt[cur];
+            f32x16 sacc[2];
+#pragma unroll
+            for (int kh = 0; kh < 2; ++kh) {
+#pragma unroll
+                for (int v = 0; v < 16; ++v) sacc[kh][v] = 0.0f;
+                const int r = kh * 32 + (lane & 31);
+#pragma unroll
+                for (int dc = 0; dc < D / 16; ++dc) {
+                    const uint4 kf = *reinterpret_cast<const uint4 *>(K + r * D + KSwz<D>(r, dc * 2 + hf) * 8);
+                    sacc[kh] = Mfma<DT>(kf, qf[dc], sacc[kh]);
+                }
+            }
+
+            float mloc = -INFINITY;
+            const bool diag = kv0 + kKvBlk - 1 > q0 + wave * 32 || kv0 + kKvBlk > p.S;
+#pragma unroll
+            for (int kh = 0; kh < 2; ++kh)
+#pragma unroll
+                for (int v = 0; v < 16; ++v) {
+                    float s = sacc[kh][v] * p.scale_log2;
+                    if (diag) {
+                        const int kv = kv0 + kh * 32 + 8 * (v >> 2) + 4 * hf + (v & 3);
+                        if (kv > qrow || kv >= p.S) s = -INFINITY;
+                    }
+                    sacc[kh][v] = s;
+                    mloc = fmaxf(mloc, s);
+                }
+            mloc = fmaxf(mloc, __shfl_xor(mloc, 32, 64));
+            const float mnew = fmaxf(m, mloc);
+            const float msub = mnew == -INFINITY ? 0.0f : mnew;
+            const float alpha = exp2f(m - msub);
+            float lsum = 0.0f;
+#pragma unroll
+            for (int kh = 0; kh < 2; ++kh)
+#pragma unroll
+                for (int v = 0; v < 16; ++v) {
+                    const float pv = exp2f(sacc[kh][v] - msub);
+                    sacc[kh][v] = pv;
+                    lsum += pv;
+                }
+            l = l * alpha + lsum;
+            m = mnew;
+#pragma unroll
+            for (int b = 0; b < DBLK; ++b)
+#pragma unroll
+                for (int v = 0; v < 16; ++v) oacc[b][v] *= alpha;
+
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                const int kh = c >> 1;
+                const int vb = (c & 1) * 8;
+                uint32_t pw[4];
+#pragma unroll
+                for (int s = 0; s < 4; ++s) {
+                    pw[s] = uint32_t(Elem<DT>::Store(sacc[kh][vb + 2 * s])) |
+                            (uint32_t(Elem<DT>::Store(sacc[kh][vb + 2 * s + 1])) << 16);
+                }
+                const uint4 pf = make_uint4(pw[0], pw[1], pw[2], pw[3]);
+#pragma unroll
+                for (int b = 0; b < DBLK; ++b) {
+                    const int d = b * 32 + (lane & 31);
+                    const uint4 vf = *reinterpret_cast<const uint4 *>(V + d * kKvBlk + (((2 * c + hf) ^ VSwz(d)) * 8));
+                    oacc[b] = Mfma<DT>(vf, pf, oacc[b]);
+                }
+            }
+        }
+        if (more) store(cur ^ 1);  // the other buffer was last read before the previous barrier
         __syncthreads();
-        if (kv0 > wave_q_hi) continue;  // block entirely in this wave's future
-
-        f32x16 sacc[2];
-#pragma unroll
-        for (int kh = 0; kh < 2; ++kh) {
-#pragma unroll
-            for (int v = 0; v < 16; ++v) sacc[kh][v] = 0.0f;
-            const int r = kh * 32 + (lane & 31);
-#pragma unroll
-            for (int dc = 0; dc < D / 16; ++dc) {
-                const uint4 kf = *reinterpret_cast<const uint4 *>(Ks + r * D + KSwz<D>(r, dc * 2 + hf) * 8);
-                sacc[kh] = Mfma<DT>(kf, qf[dc], sacc[kh]);
-            }
-        }
-
-        float mloc = -INFINITY;
-#pragma unroll
-        for (int kh = 0; kh < 2; ++kh)
-#pragma unroll
-            for (int v = 0; v < 16; ++v) {
-                const int kv = kv0 + kh * 32 + 8 * (v >> 2) + 4 * hf + (v & 3);
-                float s = sacc[kh][v] * p.scale_log2;
-                if (kv > qrow || kv >= p.S) s = -INFINITY;
-                sacc[kh][v] = s;
-                mloc = fmaxf(mloc, s);
-            }
-        mloc = fmaxf(mloc, __shfl_xor(mloc, 32, 64));
-        const float mnew = fmaxf(m, mloc);
-        const float msub = mnew == -INFINITY ? 0.0f : mnew;
-        const float alpha = exp2f(m - msub);
-        float lsum = 0.0f;
-#pragma unroll
-        for (int kh = 0; kh < 2; ++kh)
-#pragma unroll
-            for (int v = 0; v < 16; ++v) {
-                const float pv = exp2f(sacc[kh][v] - msub);
-                sacc[kh][v] = pv;
-                lsum += pv;
-            }
-        l = l * alpha + lsum;
-        m = mnew;
-#pragma unroll
-        for (int b = 0; b < DBLK; ++b)
-#pragma unroll
-            for (int v = 0; v < 16; ++v) oacc[b][v] *= alpha;
-
-#pragma unroll
-        for (int c = 0; c < 4; ++c) {
-            const int kh = c >> 1;
-            const int vb = (c & 1) * 8;
-            uint32_t pw[4];
-#pragma unroll
-            for (int s = 0; s < 4; ++s) {
-                pw[s] = uint32_t(Elem<DT>::Store(sacc[kh][vb + 2 * s])) |
-                        (uint32_t(Elem<DT>::Store(sacc[kh][vb + 2 * s + 1])) << 16);
-            }
-            const uint4 pf = make_uint4(pw[0], pw[1], pw[2], pw[3]);
-#pragma unroll
-            for (int b = 0; b < DBLK; ++b) {
-                const int d = b * 32 + (lane & 31);
-                const uint2 lo = *reinterpret_cast<const uint2 *>(Vt + d * kKvBlk + VSwz(d, 4 * c + hf) * 4);
-                const uint2 hi = *reinterpret_cast<const uint2 *>(Vt + d * kKvBlk + VSwz(d, 4 * c + 2 + hf) * 4);
-                oacc[b] = Mfma<DT>(make_uint4(lo.x, lo.y, hi.x, hi.y), pf, oacc[b]);
-            }
-        }
     }
 
     l += __shfl_xor(l, 32, 64);
@@ -246,7 +294,7 @@ void AttnLaunch(int dtype, const void *q, int64_t ldq, const void *k, int64_t ld
     p.HQ = HQ;
     p.HKV = HKV;
     p.scale_log2 = scale * 1.4426950408889634f;
-    const dim3 grid((S + kQBlk - 1) / kQBlk, HQ);
+    const dim3 grid(unsigned((S + kQBlk - 1) / kQBlk) * unsigned(HQ));
     const bool bf = dtype == kBF16;
     if (dtype != kBF16 && dtype != kF16) throw std::runtime_error("attention: dtype must be bf16 or f16");
     if (D == 128) {
