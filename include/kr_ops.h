@@ -76,12 +76,15 @@ const char *kr_ops_last_error(void);
 
 /* C[M,N] = A[M,K] . Bt[N,K]^T (+ bias[N], rounded as matmul-then-add);
  * bf16/f16 in and out, fp32 accumulate. bm = M tile (0 = automatic; 64,
- * 128 or 256). pub may be NULL.
+ * 128 or 256). pub may be NULL. wait may be NULL; else every workgroup waits
+ * for the producer tiles covering its rows of A before loading them (the
+ * GEMM as a relay consumer), and the launch consumes wait->adv_lo..adv_hi.
  * Replaces aclnnMatmul (reference exec/qwen_main.cpp:499-512,
- * exec/runtime/op_impl.cpp:175-201) and the fused QKV bias Add (:1336-1344). */
+ * exec/runtime/op_impl.cpp:175-201) and the fused QKV bias Add (:1336-1344);
+ * the wait replaces a kr_wait_aic launch ahead of it (qwen_main.cpp:672-688). */
 int kr_op_gemm(int dtype, const void *A, int64_t lda, const void *Bt, int64_t ldb, void *C,
-               int64_t ldc, const void *bias, int M, int N, int K, int bm, const kr_pub *pub,
-               void *stream);
+               int64_t ldc, const void *bias, int M, int N, int K, int bm, const kr_wait *wait,
+               const kr_pub *pub, void *stream);
 
 /* Elementwise op on [rows, cols]; x1 used by mul/add/swiglu; dtype_out
  * differs from dtype_in only for cast. tile_rows = relay granularity
@@ -129,6 +132,15 @@ int kr_op_attention(int dtype, const void *q, int64_t ldq, const void *k, int64_
 /* dst[C,R] = src[R,C]^T for 16-bit elements (weight re-layout at load; the
  * reference stores matmul weights as weight_t [K,N], scripts/export_model.py:159-161). */
 int kr_op_transpose(const void *src, void *dst, int R, int C, void *stream);
+
+/* A stream with a hardware queue of its own (CU-masked to every CU). Two
+ * relay parties that wait on each other on the device must not share a queue
+ * (a queue runs its kernels in order); ordinary streams are multiplexed onto
+ * a few queues. Returns NULL on failure. No reference counterpart: the
+ * reference's two streams feed separate AIC and AIV engines
+ * (exec/qwen_main.cpp:206-209). */
+void *kr_op_stream_create(void);
+int kr_op_stream_destroy(void *stream);
 
 #ifdef __cplusplus
 }

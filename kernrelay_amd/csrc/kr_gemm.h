@@ -17,10 +17,14 @@ struct GemmDesc {
     int bm = 0;                  // M tile (0 = pick automatically)
     int bn = 0;                  // N tile (0 = pick automatically)
     RelayPub pub{};              // pub.ctrl == nullptr: no release
+    RelayWait wait{};            // wait.ctrl == nullptr: A is ready; else each
+                                 // workgroup waits for the tiles of A it reads
 };
 
 // Launch C = A . Bt^T (+bias). pub.rows_per_tile (when publishing) must be a
-// multiple of the chosen M tile; pub.arrivals is computed here.
+// multiple of the chosen M tile; pub.arrivals is computed here. With a wait,
+// every workgroup first waits for the producer tiles covering its rows of A,
+// and the launch consumes wait.adv_lo..adv_hi once all workgroups are done.
 void GemmLaunch(const GemmDesc &d, hipStream_t stream);
 
 struct GemmTile {

@@ -45,36 +45,41 @@ struct GemmParams {
     int64_t lda, ldb, ldc;
     int M, N, K;
     int tiles_m, tiles_n;
+    int order_rows;  // > 0: dispatch tiles in relay-tile order, this many rows each
     RelayPub pub;
+    RelayWait wait;
 };
 
 __device__ __forceinline__ int Swz(int row, int chunk) { return chunk ^ ((row >> 1) & 7); }
 
 // Workgroup -> output tile. The dispatcher deals workgroups to the 8 XCDs
-// round-robin (XCD = blockIdx % 8) and each XCD has its own L2.
-// * No relay: XCD x takes a contiguous run of tile ids and walks it
-//   column-major (row blocks fastest), so a weight column block is read by
-//   consecutive workgroups of one XCD while it sits in that XCD's L2.
-// * Relay: relay tiles are dispatched front to back (each must complete as
-//   early as possible); inside a relay tile the order is column-major so its
-//   row blocks share each weight block.
-__device__ __forceinline__ void TileOf(int bid, int tiles_m, int tiles_n, int bm, const RelayPub &pub, int &tm,
-                                       int &tn)
+// round-robin (XCD = blockIdx % 8) and each XCD has its own L2. Within a run
+// of `per` consecutive workgroup ids starting at `first`, XCD x takes a
+// contiguous chunk of the run's tiles (row blocks fastest), so a weight column
+// block is read by workgroups of one XCD while it sits in that XCD's L2.
+// * No relay: one run over all tiles.
+// * Relay (order_rows > 0): one run per relay tile, front to back, so tile 0
+//   of the rows is complete first; each run covers order_rows/bm row blocks.
+__device__ __forceinline__ int XcdChunk(int bid, int first, int per)
 {
-    if (pub.ctrl != nullptr) {
-        const int mt = pub.rows_per_tile / bm;  // row blocks per relay tile
+    const int off = (bid - first) & 7;
+    const int slot = (bid - first) >> 3;
+    const int q = per >> 3, rem = per & 7;
+    return off < rem ? off * (q + 1) + slot : rem * (q + 1) + (off - rem) * q + slot;
+}
+
+__device__ __forceinline__ void TileOf(int bid, int tiles_m, int tiles_n, int bm, int order_rows, int &tm, int &tn)
+{
+    if (order_rows > 0) {
+        const int mt = order_rows / bm;  // row blocks per relay tile
         const int per = mt * tiles_n;
         const int r = bid / per;
-        const int local = bid - r * per;
-        tm = r * mt + local % mt;
-        tn = local / mt;
+        const int t = XcdChunk(bid, r * per, per);
+        tm = r * mt + t % mt;
+        tn = t / mt;
         return;
     }
-    const int T = tiles_m * tiles_n;
-    const int xcd = bid & 7;
-    const int slot = bid >> 3;
-    const int q = T >> 3, rem = T & 7;
-    const int t = xcd < rem ? xcd * (q + 1) + slot : rem * (q + 1) + (xcd - rem) * q + slot;
+    const int t = XcdChunk(bid, 0, tiles_m * tiles_n);
     tm = t % tiles_m;
     tn = t / tiles_m;
 }
@@ -96,7 +101,8 @@ __device__ __forceinline__ f32x16 Mfma(const uint4 &a, const uint4 &b, const f32
 // col 8*(v/4) + 4*(l/32) + v%4. Each run of 4 columns goes to LDS as one
 // 8-byte write into a row-major tile whose 8-byte slots are XOR-swizzled with
 // row & 31 (32 rows of one column run hit 32 distinct bank pairs); then every
-// thread copies 16-byte row chunks to C (8 lanes cover a 128-byte line).
+// thread copies 16-byte row chunks to C (8 lanes cover a 128-byte line),
+// with device-scope stores when the launch releases relay tiles.
 // `stage` must hold BM*BN 16-bit values and be free (all waves past their
 // last LDS read of the main loop).
 template <int DT, int BM, int BN, int MI, int NI>
@@ -135,6 +141,7 @@ __device__ __forceinline__ void StoreTile(const GemmParams &p, f32x16 (&acc)[MI]
     __syncthreads();
     constexpr int CPR = BN / 8;  // 16-byte chunks per row
     const bool vec = (p.ldc % 8 == 0) && ((reinterpret_cast<uintptr_t>(p.C) & 15) == 0);
+    const bool coh = p.pub.ctrl != nullptr;  // released tiles: device-scope stores
 #pragma unroll 4
     for (int idx = threadIdx.x; idx < BM * CPR; idx += kThreads) {
         const int row = idx / CPR;
@@ -146,12 +153,12 @@ __device__ __forceinline__ void StoreTile(const GemmParams &p, f32x16 (&acc)[MI]
         if (row & 1) v = make_uint4(v.z, v.w, v.x, v.y);
         uint16_t *dst = p.C + int64_t(gm) * p.ldc + gn;
         if (vec && gn + 8 <= p.N) {
-            *reinterpret_cast<uint4 *>(dst) = v;
+            PutU128(dst, v, coh);
         } else {
             const uint32_t w[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
             for (int e = 0; e < 8; ++e)
-                if (gn + e < p.N) dst[e] = uint16_t(w[e >> 1] >> ((e & 1) * 16));
+                if (gn + e < p.N) PutU16(dst + e, uint16_t(w[e >> 1] >> ((e & 1) * 16)), coh);
         }
     }
 }
@@ -176,9 +183,10 @@ GemmKernel(GemmParams p)
     const int wn = wave & 1;
 
     int tm, tn;
-    TileOf(blockIdx.x, p.tiles_m, p.tiles_n, BM, p.pub, tm, tn);
+    TileOf(blockIdx.x, p.tiles_m, p.tiles_n, BM, p.order_rows, tm, tn);
     const int m0 = tm * BM;
     const int n0 = tn * BN;
+    RelayWaitRows(p.wait, m0, min(m0 + BM, p.M));
 
     const int lrow = tid >> 3;       // 0..31
     const int lchunk = tid & 7;
@@ -271,6 +279,7 @@ GemmKernel(GemmParams p)
 
     StoreTile<DT, BM, BN>(p, acc, smem, m0, n0, wm, wn, lane);
     if (p.pub.ctrl != nullptr) RelayArrive(p.pub, m0 / p.pub.rows_per_tile);
+    RelayFinish(p.wait);
 }
 
 // ---------------------------------------------------------------------------
@@ -304,9 +313,15 @@ void LaunchTyped(const GemmParams &base, hipStream_t stream)
     GemmParams p = base;
     p.tiles_m = (p.M + BM - 1) / BM;
     p.tiles_n = (p.N + BN - 1) / BN;
+    // relay order needs whole relay tiles of whole row blocks
+    auto whole = [&](int rows) { return rows > 0 && rows % BM == 0 && p.tiles_m % (rows / BM) == 0; };
+    p.order_rows = 0;
     if (p.pub.ctrl != nullptr) {
-        if (p.pub.rows_per_tile % BM != 0) throw std::runtime_error("relay tile rows not a multiple of BM");
+        if (!whole(p.pub.rows_per_tile)) throw std::runtime_error("relay tile rows must be a multiple of BM dividing M");
         p.pub.arrivals = (p.pub.rows_per_tile / BM) * p.tiles_n;
+        p.order_rows = p.pub.rows_per_tile;
+    } else if (p.wait.ctrl != nullptr && p.wait.row_off == 0 && whole(p.wait.prod_rows)) {
+        p.order_rows = p.wait.prod_rows;  // the rows that are released first run first
     }
     const dim3 grid(p.tiles_m * p.tiles_n);
     if (p.K % kPipeK == 0 && !ForceSimple()) {
@@ -374,6 +389,8 @@ void GemmLaunch(const GemmDesc &d, hipStream_t stream)
     p.N = d.N;
     p.K = d.K;
     p.pub = d.pub;
+    p.wait = d.wait;
+    if (p.wait.ctrl != nullptr && p.wait.prod_rows <= 0) throw std::runtime_error("gemm: wait.prod_rows must be > 0");
     const int relay_rows = d.pub.ctrl != nullptr ? d.pub.rows_per_tile : 0;
     GemmTile t = GemmPickTile(d.M, d.N, relay_rows);
     if (const char *e = std::getenv("KR_GEMM_TILE")) {

@@ -2,6 +2,9 @@
 #include "../../include/kr_ops.h"
 
 #include <string>
+#include <vector>
+
+#include <hip/hip_ext.h>
 
 #include "kr_gemm.h"
 #include "kr_misc.h"
@@ -66,7 +69,7 @@ extern "C" {
 const char *kr_ops_last_error(void) { return g_last_error.c_str(); }
 
 int kr_op_gemm(int dtype, const void *A, int64_t lda, const void *Bt, int64_t ldb, void *C, int64_t ldc,
-               const void *bias, int M, int N, int K, int bm, const kr_pub *pub, void *stream)
+               const void *bias, int M, int N, int K, int bm, const kr_wait *wait, const kr_pub *pub, void *stream)
 {
     return Guard([&] {
         kr::GemmDesc d;
@@ -83,6 +86,7 @@ int kr_op_gemm(int dtype, const void *A, int64_t lda, const void *Bt, int64_t ld
         d.K = K;
         d.bm = bm;
         d.pub = ToPub(pub);
+        d.wait = ToWait(wait);
         if (d.pub.ctrl && M % d.pub.rows_per_tile != 0) throw std::runtime_error("gemm: M must be a multiple of rows_per_tile");
         kr::GemmLaunch(d, S(stream));
     });
@@ -171,6 +175,26 @@ int kr_op_attention(int dtype, const void *q, int64_t ldq, const void *k, int64_
 int kr_op_transpose(const void *src, void *dst, int R, int C, void *stream)
 {
     return Guard([&] { kr::TransposeLaunch(src, dst, R, C, S(stream)); });
+}
+
+void *kr_op_stream_create(void)
+{
+    hipStream_t st = nullptr;
+    const int rc = Guard([&] {
+        int dev = 0;
+        kr::Check(hipGetDevice(&dev), "hipGetDevice");
+        hipDeviceProp_t prop;
+        kr::Check(hipGetDeviceProperties(&prop, dev), "device props");
+        std::vector<uint32_t> all((prop.multiProcessorCount + 31) / 32, 0u);
+        for (int c = 0; c < prop.multiProcessorCount; ++c) all[c / 32] |= 1u << (c % 32);
+        kr::Check(hipExtStreamCreateWithCUMask(&st, uint32_t(all.size()), all.data()), "create stream");
+    });
+    return rc == 0 ? static_cast<void *>(st) : nullptr;
+}
+
+int kr_op_stream_destroy(void *stream)
+{
+    return Guard([&] { kr::Check(hipStreamDestroy(static_cast<hipStream_t>(stream)), "destroy stream"); });
 }
 
 }  // extern "C"

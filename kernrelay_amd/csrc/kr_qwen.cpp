@@ -136,7 +136,8 @@ public:
     {
         const auto t0 = Clock::now();
         Check(hipSetDevice(device_), "hipSetDevice");
-        streams_.Create(device_);
+        // the split gives the consumer stream its own CUs (see BuildSplit)
+        streams_.Create(device_, mode_.split ? std::max(1, EnvInt("KR_SPLIT_CUS_PER_XCD", 2)) : 0);
         Check(hipEventCreate(&t0_), "event");
         Check(hipEventCreate(&tp_), "event");
         Check(hipEventCreate(&tc_), "event");
@@ -569,7 +570,7 @@ private:
     }
 
     void Gemm(int s, const void *A, int64_t lda, const uint16_t *Bt, int N, int K, void *C, int64_t ldc,
-              const uint16_t *bias, int M, RelayPub pub)
+              const uint16_t *bias, int M, RelayPub pub, RelayWait wait = RelayWait{})
     {
         GemmDesc d;
         d.dtype = kBF16;
@@ -584,6 +585,7 @@ private:
         d.N = N;
         d.K = K;
         d.pub = pub;
+        d.wait = wait;
         Emit(s, [d](hipStream_t st) { GemmLaunch(d, st); });
     }
 
@@ -636,17 +638,150 @@ private:
         Emit(s, [d](hipStream_t st) { RowLaunch(d, st); });
     }
 
+    // ---------------------------------------------------------- relay split
+    // SwiGLU over rows [r0, r0+rows) of the interleaved gate/up output.
+    void SwigluRows(int s, int r0, int rows, RelayPub pub, int grid = 0)
+    {
+        EwDesc e;
+        e.op = kEwSwigluGU;
+        e.x0 = gu_.as<uint16_t>() + size_t(r0) * 2 * I_;
+        e.y = act_.as<uint16_t>() + size_t(r0) * I_;
+        e.rows = rows;
+        e.cols = I_;
+        e.pub = pub;
+        e.grid = grid;
+        Emit(s, [e](hipStream_t st) { EwLaunch(e, st); });
+    }
+
+    // qkv GEMM (+bias), qk-norm, RoPE and attention of layer l on stream P.
+    void EmitAttention(int P, int l, RelayWait qkv_wait)
+    {
+        const Layer &w = layers_[l];
+        const int S = seq_;
+        const int64_t ld = ldqkv_;
+        uint16_t *qkv = qkv_.as<uint16_t>();
+        Gemm(P, x_.get(), H_, w.qkv, int(ld), H_, qkv, ld, w.bias, S, RelayPub{}, qkv_wait);
+        uint16_t *q = qkv, *kk = qkv + size_t(HQ_) * D_, *v = qkv + size_t(HQ_ + HKV_) * D_;
+        int64_t ldq = ld, ldk = ld;
+        if (qk_norm_) {
+            RmsNorm(P, q, w.qn, qn_.get(), S * HQ_, D_, HQ_, ld);
+            RmsNorm(P, kk, w.kn, kn_.get(), S * HKV_, D_, HKV_, ld);
+            q = qn_.as<uint16_t>();
+            kk = kn_.as<uint16_t>();
+            ldq = int64_t(HQ_) * D_;
+            ldk = int64_t(HKV_) * D_;
+        }
+        const int HQ = HQ_, HKV = HKV_, D = D_;
+        const uint16_t *cs = cos_, *sn = sin_;
+        Emit(P, [=](hipStream_t st) {
+            RopeLaunch(kBF16, q, ldq, S, HQ, D, cs, sn, st);
+            RopeLaunch(kBF16, kk, ldk, S, HKV, D, cs, sn, st);
+        });
+        uint16_t *attn = attn_.as<uint16_t>();
+        const float scale = float(1.0 / std::sqrt(double(D_)));
+        Emit(P, [=](hipStream_t st) {
+            AttnLaunch(kBF16, q, ldq, kk, ldk, v, ld, attn, int64_t(HQ) * D, S, HQ, HKV, D, scale, st);
+        });
+    }
+
+    // relay_split[:k] — the MI355X form of the reference's AIC/AIV relay.
+    // The producer stream P runs on most CUs, the consumer stream C on a
+    // disjoint partition (KR_SPLIT_CUS_PER_XCD, default 2 per XCD; P keeps
+    // 240 of 256, which leaves the wave count of every GEMM of the 7B layer
+    // unchanged; a 256x256 GEMM workgroup needs a whole CU, and consumer
+    // workgroups interleaved onto the producer's CUs starve both).
+    // * The gate/up GEMM releases its k row tiles as they complete.
+    // * C holds one resident SwiGLU consumer for the whole prefill: for every
+    //   layer it takes tiles 0..kc-1 (kc = KR_SPLIT_C_TILES, default k-1) as
+    //   they are released and releases its act tiles, while P still computes
+    //   the later gate/up tiles.
+    // * P runs SwiGLU on the remaining tiles itself at full width right after
+    //   the GEMM, then waits for C's act tiles and runs down.
+    // Edges behind single-wave producers (o, down -> Add+RMSNorm) release all
+    // their tiles at once, so they stay in P's stream order. Every row goes
+    // through the same arithmetic as in the serial schedule: identical bits.
+    void BuildSplit()
+    {
+        const int S = seq_;
+        const int k = mode_.tiles;
+        const int T = S / k;
+        const int kc = std::max(0, std::min(k - 1, EnvInt("KR_SPLIT_C_TILES", k - 1)));
+        const int P = 0, C = 1;
+        // block (l, t) of each edge = base + l*k + t
+        const int gu_act = NewEdge(k * L_), act_down = NewEdge(k * L_);
+        ctrl_.Alloc(std::max<size_t>(ctrl_blocks_, 1) * kWords * 4);
+        Check(hipMemset(ctrl_.get(), 0, ctrl_.bytes()), "zero ctrl");
+        max_spins_ = uint32_t(EnvInt("KR_MAX_SPINS", int(kDefaultMaxSpins)));
+
+        if (kc > 0) {
+            SwigluRelayDesc d;
+            d.gu = gu_.get();
+            d.act = act_.get();
+            d.cols = I_;
+            d.tile_rows = T;
+            d.tiles = k;
+            d.kc = kc;
+            d.layers = L_;
+            d.ctrl = ctrl_.as<int32_t>();
+            d.in0 = gu_act;
+            d.out0 = act_down;
+            d.max_spins = max_spins_;
+            d.cus = streams_.cons_cus;
+            for (int l = 0; l < L_; ++l)
+                for (int t = 0; t < kc; ++t) consumed_.push_back(gu_act + l * k + t);
+            Emit(C, [d](hipStream_t st) { SwigluRelayLaunch(d, st); });
+        }
+
+        uint16_t *h0 = h_[0].as<uint16_t>(), *h1 = h_[1].as<uint16_t>();
+        uint16_t *x = x_.as<uint16_t>();
+        {
+            const void *tab = embed_;
+            const int64_t *ids = ids_.as<int64_t>();
+            const int H = H_;
+            const int64_t V = V_;
+            Emit(P, [=](hipStream_t st) { EmbedLaunch(tab, ids, h0, S, H, V, st); });
+            RmsNorm(P, h0, layers_[0].ln1, x, S, H_, 1, 0);
+        }
+        uint16_t *hcur = h0, *hnxt = h1;
+        for (int l = 0; l < L_; ++l) {
+            const Layer &w = layers_[l];
+            EmitAttention(P, l, RelayWait{});
+            Gemm(P, attn_.get(), int64_t(HQ_) * D_, w.o, H_, HQ_ * D_, o_.get(), H_, nullptr, S, RelayPub{});
+            AddRmsNorm(P, hcur, o_.get(), w.ln2, x, hnxt, RelayWait{}, 0, RelayPub{}, 0);
+            // gate/up releases its k row tiles; SwiGLU: tiles < kc on C, the rest here
+            Gemm(P, x, H_, w.gu, 2 * I_, H_, gu_.get(), 2 * int64_t(I_), nullptr, S,
+                 kc > 0 ? Pub(gu_act + l * k, T) : RelayPub{});
+            SwigluRows(P, kc * T, (k - kc) * T, RelayPub{});
+            if (kc > 0) {
+                RelayWait wd = WaitDesc(act_down + l * k, k);
+                wd.adv_hi = kc;
+                for (int t = 0; t < kc; ++t) consumed_.push_back(act_down + l * k + t);
+                Emit(P, [wd, T, kc](hipStream_t st) { WaitLaunch(wd, 0, kc * T, st); });
+            }
+            Gemm(P, act_.get(), I_, w.down, H_, I_, down_.get(), H_, nullptr, S, RelayPub{});
+            const bool last = l + 1 == L_;
+            AddRmsNorm(P, hnxt, down_.get(), last ? final_norm_ : layers_[l + 1].ln1, last ? xf_.get() : x_.get(),
+                       last ? hf_.get() : static_cast<void *>(hcur), RelayWait{}, 0, RelayPub{}, 0);
+        }
+        Gemm(P, xf_.get(), H_, lm_, V_, H_, logits_.get(), V_, nullptr, S, RelayPub{});
+    }
+
     void BuildProgram()
     {
         const int S = seq_;
-        const int k = mode_.split ? mode_.tiles : 1;
-        if (mode_.split && (S % k != 0 || (S / k) % 64 != 0))
-            throw std::runtime_error("relay_split: seq/tiles must be a multiple of 64");
-        relay_grid_ = EnvInt("KR_RELAY_GRID", 64);
+        if (mode_.split) {
+            if (S % mode_.tiles != 0 || (S / mode_.tiles) % 64 != 0)
+                throw std::runtime_error("relay_split: seq/tiles must be a multiple of 64");
+            BuildSplit();
+            return;
+        }
+        // Unsplit relay modes: one tile per edge, the whole-op release of the
+        // reference's BuildDual (qwen_main.cpp:811-923).
+        const int k = 1;
         max_spins_ = uint32_t(EnvInt("KR_MAX_SPINS", int(kDefaultMaxSpins)));
         const int P = 0, C = 1;
-        // Six edges per layer, each of k relay blocks (block t = producer tile
-        // t's flag and the single consumer's state for it).
+        // Six edges per layer (block = the producer's flag and the single
+        // consumer's state for it).
         struct LayerEdges { int o_ln2, ln2_gu, gu_act, act_down, down_ln, exit; };
         std::vector<LayerEdges> le(L_);
         if (mode_.dual)
@@ -656,19 +791,14 @@ private:
             ctrl_.Alloc(std::max<size_t>(ctrl_blocks_, 1) * kWords * 4);
             Check(hipMemset(ctrl_.get(), 0, ctrl_.bytes()), "zero ctrl");
         }
-        const int rows_tile = S / k;
-        const int cgrid = mode_.split ? relay_grid_ : 0;
-        const int ctile = mode_.split ? rows_tile : 0;
+        const int rows_tile = S;
+        const int cgrid = 0;
+        const int ctile = 0;
 
-        // Consumer-side wait on a producer edge: in-kernel per tile (split),
-        // else a whole-edge wait ahead of the consumer.
+        // Consumer-side wait on a producer edge: a whole-edge wait ahead of
+        // the consumer.
         auto consumer_wait = [&](int edge) -> RelayWait {
-            if (!mode_.dual) return RelayWait{};
-            if (mode_.split) {
-                for (int t = 0; t < k; ++t) consumed_.push_back(edge + t);
-                return WaitDesc(edge, k);
-            }
-            WaitBefore(C, edge, 1);
+            if (mode_.dual) WaitBefore(C, edge, 1);
             return RelayWait{};
         };
         auto release = [&](int edge) { return mode_.dual ? Pub(edge, rows_tile) : RelayPub{}; };
@@ -687,35 +817,10 @@ private:
             RmsNorm(P, h0, layers_[0].ln1, x, S, H_, 1, 0);
         }
         uint16_t *hcur = h0, *hnxt = h1;
-        const int64_t ld = ldqkv_;
         for (int l = 0; l < L_; ++l) {
             const Layer &w = layers_[l];
             if (mode_.dual && l > 0) WaitBefore(P, le[l - 1].exit, k);
-            uint16_t *qkv = qkv_.as<uint16_t>();
-            Gemm(P, x, H_, w.qkv, int(ld), H_, qkv, ld, w.bias, S, RelayPub{});
-            uint16_t *q = qkv, *kk = qkv + size_t(HQ_) * D_, *v = qkv + size_t(HQ_ + HKV_) * D_;
-            int64_t ldq = ld, ldk = ld;
-            if (qk_norm_) {
-                RmsNorm(P, q, w.qn, qn_.get(), S * HQ_, D_, HQ_, ld);
-                RmsNorm(P, kk, w.kn, kn_.get(), S * HKV_, D_, HKV_, ld);
-                q = qn_.as<uint16_t>();
-                kk = kn_.as<uint16_t>();
-                ldq = int64_t(HQ_) * D_;
-                ldk = int64_t(HKV_) * D_;
-            }
-            {
-                const int HQ = HQ_, HKV = HKV_, D = D_;
-                const uint16_t *cs = cos_, *sn = sin_;
-                Emit(P, [=](hipStream_t st) {
-                    RopeLaunch(kBF16, q, ldq, S, HQ, D, cs, sn, st);
-                    RopeLaunch(kBF16, kk, ldk, S, HKV, D, cs, sn, st);
-                });
-                uint16_t *attn = attn_.as<uint16_t>();
-                const float scale = float(1.0 / std::sqrt(double(D_)));
-                Emit(P, [=](hipStream_t st) {
-                    AttnLaunch(kBF16, q, ldq, kk, ldk, v, ld, attn, int64_t(HQ) * D, S, HQ, HKV, D, scale, st);
-                });
-            }
+            EmitAttention(P, l, RelayWait{});
             // o_proj -> Add+RMSNorm(post_attention_layernorm)
             Gemm(P, attn_.get(), int64_t(HQ_) * D_, w.o, H_, HQ_ * D_, o_.get(), H_, nullptr, S,
                  release(le[l].o_ln2));
@@ -805,7 +910,6 @@ private:
     std::vector<int> consumed_;
     std::map<int, hipEvent_t> edge_event_;
     std::vector<hipEvent_t> events_;
-    int relay_grid_ = 64;
     uint32_t max_spins_ = kDefaultMaxSpins;
     hipEvent_t t0_ = nullptr, tp_ = nullptr, tc_ = nullptr;
     std::vector<double> samples_, host_samples_, dev_samples_;

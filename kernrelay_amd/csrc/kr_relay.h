@@ -23,9 +23,12 @@
 // kernels/kr_wait_aiv.cpp:7-36). Here the release is folded into the
 // producer's epilogue (every workgroup arrives; the last one releases) and
 // the wait into the consumer's prologue (one lane spins on an agent-scope load
-// with s_sleep backoff, then a workgroup barrier). Cross-XCD visibility comes
-// from agent-scope release/acquire: the release fence writes this XCD's L2
-// back to memory, the acquire fence invalidates the consumer's caches.
+// with s_sleep backoff, then a workgroup barrier). Cross-XCD visibility: the
+// producer writes released data with device-scope stores and arrives only
+// once they are acknowledged (no cache-wide write-back, see RelayArrive); a
+// consumer that waits inside its own kernel takes an agent-scope acquire
+// (its XCD's caches may hold stale lines of the buffer), and a consumer
+// launched behind a wait kernel gets the acquire of its own kernel start.
 #pragma once
 
 #include "kr_common.h"
@@ -122,8 +125,11 @@ __device__ __forceinline__ void RelayFinish(const RelayWait &w)
     if (w.ctrl == nullptr || w.adv_hi <= w.adv_lo) return;
     __syncthreads();
     if (threadIdx.x == 0) {
+        // relaxed is enough: this workgroup's waits (the loads of `consumed`
+        // it spun on) have completed before its ticket, and the counters are
+        // next read by waiters of a later launch or by the host.
         int32_t *ticket = w.ctrl + size_t(w.state0 + w.adv_lo) * kWords + kOffDone;
-        const int32_t t = __hip_atomic_fetch_add(ticket, 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+        const int32_t t = __hip_atomic_fetch_add(ticket, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         if (t == int32_t(gridDim.x * gridDim.y * gridDim.z) - 1) {
             StoreRelaxed(ticket, 0);
             for (int k = w.adv_lo; k < w.adv_hi; ++k) {
@@ -134,24 +140,66 @@ __device__ __forceinline__ void RelayFinish(const RelayWait &w)
                 StoreRelaxed(st + kOffConsumed, c + 1);
                 StoreRelaxed(st + kOffStatus, to ? 2 : 1);
             }
-            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
         }
     }
 }
 
-// Every thread calls this after the workgroup's stores for tile `tile` have
-// been issued. The last arriving workgroup releases the tile.
+// Stores of data a relay releases. A producer that publishes writes its
+// outputs with device-scope stores (sc1: written through this XCD's L2 to
+// memory, where every XCD reads it), so a release needs no cache-wide
+// operation: an agent-scope release fence would write back the whole L2 of
+// the XCD (buffer_wbl2) once per workgroup, and the consumer's matching
+// acquire would invalidate the L2 that a concurrently running GEMM relies on
+// for operand reuse. Ordinary stores when `coherent` is false (no release).
+typedef uint32_t RelayU32x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ void PutU128(void *p, uint4 v, bool coherent)
+{
+    if (coherent) {
+        const RelayU32x4 w = {v.x, v.y, v.z, v.w};
+        // a store of more than 8 bytes reads its data VGPRs after issue: two
+        // wait states before anything may overwrite them (the compiler cannot
+        // see into the asm to insert them itself)
+        asm volatile("global_store_dwordx4 %0, %1, off sc1\n\ts_nop 1" ::"v"(p), "v"(w) : "memory");
+    } else {
+        *reinterpret_cast<uint4 *>(p) = v;
+    }
+}
+
+__device__ __forceinline__ void PutU32(void *p, uint32_t v, bool coherent)
+{
+    if (coherent) {
+        asm volatile("global_store_dword %0, %1, off sc1" ::"v"(p), "v"(v) : "memory");
+    } else {
+        *reinterpret_cast<uint32_t *>(p) = v;
+    }
+}
+
+__device__ __forceinline__ void PutU16(void *p, uint16_t v, bool coherent)
+{
+    if (coherent) {
+        asm volatile("global_store_short %0, %1, off sc1" ::"v"(p), "v"(uint32_t(v)) : "memory");
+    } else {
+        *reinterpret_cast<uint16_t *>(p) = v;
+    }
+}
+
+// Every thread calls this after issuing its stores for tile `tile` with the
+// Put* helpers (coherent = true). Each thread waits until its stores are
+// acknowledged at device scope, the barrier makes that true for the whole
+// workgroup, then one device-scope atomic arrives; the last arriving
+// workgroup releases the tile by bumping `published`.
 __device__ __forceinline__ void RelayArrive(const RelayPub &p, int tile)
 {
     if (p.ctrl == nullptr) return;
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this lane's stores are complete
     __syncthreads();
     if (threadIdx.x == 0) {
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
         int32_t *flag = p.ctrl + size_t(p.flag0 + tile) * kWords;
-        const int32_t t = __hip_atomic_fetch_add(flag + kOffArrive, 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+        const int32_t t = __hip_atomic_fetch_add(flag + kOffArrive, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         if (t == p.arrivals - 1) {
             StoreRelaxed(flag + kOffArrive, 0);
-            __hip_atomic_fetch_add(flag + kOffPublished, 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_fetch_add(flag + kOffPublished, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
     }
 }

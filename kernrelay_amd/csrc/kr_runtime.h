@@ -96,14 +96,22 @@ inline uint32_t NodeSeed(const std::string &id, uint32_t rank)
 // CU mask that keeps `per_xcd` CUs in each of the 8 XCDs whether the logical
 // CU numbering is XCD-major (CU c in XCD c/32) or XCD-interleaved (c % 8):
 // c = 32*x + ((x + 8*j) mod 32). Never leaves an XCD without a CU.
-inline std::vector<uint32_t> ConsumerCuMask(int num_cus, int per_xcd)
+// `per_xcd` CUs on every XCD. Workgroups are dealt to the 8 XCDs
+// round-robin and each XCD schedules its share on its own CUs, so a CU set
+// that missed an XCD would stall that XCD's share of every kernel launched on
+// it (the runtime refuses a queue whose mask leaves an XCD empty), and a set
+// that took more from one XCD would make it the straggler. On MI355X mask bit
+// c addresses XCD c % 8 (then shader engine, then CU within it), so bits
+// x + 8j, j < per_xcd, give every XCD per_xcd CUs on different shader
+// engines. KR_CU_LAYOUT=blocked assumes bits [x*n/8, (x+1)*n/8) on XCD x.
+inline std::vector<uint32_t> ReservedCuMask(int num_cus, int per_xcd)
 {
     std::vector<uint32_t> mask((num_cus + 31) / 32, 0u);
-    const int per_xcd_cus = num_cus / 8;
-    per_xcd = std::max(1, std::min(per_xcd, per_xcd_cus / 8 > 0 ? 4 : 1));
+    const std::string layout = EnvStr("KR_CU_LAYOUT", "interleaved");
+    const int per = num_cus / 8;
     for (int x = 0; x < 8; ++x)
-        for (int j = 0; j < per_xcd; ++j) {
-            const int c = per_xcd_cus * x + ((x + 8 * j) % per_xcd_cus);
+        for (int j = 0; j < per_xcd && j < per; ++j) {
+            const int c = layout == "blocked" ? per * x + j : x + 8 * j;
             if (c < num_cus) mask[c / 32] |= 1u << (c % 32);
         }
     return mask;
@@ -111,35 +119,44 @@ inline std::vector<uint32_t> ConsumerCuMask(int num_cus, int per_xcd)
 
 // Producer + consumer stream pair, each on its own hardware queue.
 //
-// The relay waits in both directions on the device (consumer kernels spin on
-// producer tiles, the producer's one-workgroup waits spin on consumer
-// releases), so the two streams must run concurrently. Ordinary streams are
-// multiplexed onto a few hardware queues once a process holds more streams
-// than GPU_MAX_HW_QUEUES (a torch stream pool alone creates 32): two streams on
-// one queue would run a captured producer graph to completion before the
-// consumer graph starts. A CU-masked stream always gets a queue of its own, so
-// both streams are created with explicit CU masks: the producer with every
-// CU, the consumer with every CU or, with KR_CONSUMER_CUS_PER_XCD = 1..4, a
-// few CUs per XCD so spinning consumers can only ever occupy those.
+// The relay waits in both directions on the device, so the two streams must
+// run concurrently. Ordinary streams are multiplexed onto a few hardware
+// queues once a process holds more streams than GPU_MAX_HW_QUEUES (a torch
+// stream pool alone creates 32): two streams on one queue would run a
+// captured producer graph to completion before the consumer graph starts. A
+// CU-masked stream always gets a queue of its own, so both streams are
+// created with explicit CU masks.
+// * partition_per_xcd > 0 (relay split): the consumer owns that many CUs per
+//   XCD and the producer the rest, disjoint. A 256x256 GEMM workgroup needs a
+//   whole CU; consumer workgroups interleaved onto the producer's CUs keep
+//   CUs from draining and starve both kernels, so the two engines get
+//   separate CUs as the reference's AIC/AIV cores are separate.
+// * Otherwise the producer gets every CU and the consumer every CU or, with
+//   KR_CONSUMER_CUS_PER_XCD = 1..4, a few CUs per XCD.
 struct StreamPair {
     hipStream_t prod = nullptr;
     hipStream_t cons = nullptr;
     int cons_cus = 0;  // CUs in the consumer mask
     int prod_cus = 0;
 
-    void Create(int device)
+    void Create(int device, int partition_per_xcd = 0)
     {
         hipDeviceProp_t prop;
         Check(hipGetDeviceProperties(&prop, device), "device props");
         const int ncu = prop.multiProcessorCount;
         std::vector<uint32_t> all((ncu + 31) / 32, 0u);
         for (int c = 0; c < ncu; ++c) all[c / 32] |= 1u << (c % 32);
-        Check(hipExtStreamCreateWithCUMask(&prod, uint32_t(all.size()), all.data()), "create producer stream");
-        prod_cus = ncu;
-        const int per_xcd = EnvInt("KR_CONSUMER_CUS_PER_XCD", 0);
-        std::vector<uint32_t> mask = per_xcd > 0 ? ConsumerCuMask(ncu, per_xcd) : all;
-        Check(hipExtStreamCreateWithCUMask(&cons, uint32_t(mask.size()), mask.data()), "create consumer stream");
-        for (uint32_t w : mask) cons_cus += __builtin_popcount(w);
+        std::vector<uint32_t> pmask = all, cmask = all;
+        if (partition_per_xcd > 0) {
+            cmask = ReservedCuMask(ncu, partition_per_xcd);
+            for (size_t i = 0; i < pmask.size(); ++i) pmask[i] &= ~cmask[i];
+        } else if (const int per_xcd = EnvInt("KR_CONSUMER_CUS_PER_XCD", 0); per_xcd > 0) {
+            cmask = ReservedCuMask(ncu, std::min(per_xcd, 4));
+        }
+        Check(hipExtStreamCreateWithCUMask(&prod, uint32_t(pmask.size()), pmask.data()), "create producer stream");
+        Check(hipExtStreamCreateWithCUMask(&cons, uint32_t(cmask.size()), cmask.data()), "create consumer stream");
+        for (uint32_t w : pmask) prod_cus += __builtin_popcount(w);
+        for (uint32_t w : cmask) cons_cus += __builtin_popcount(w);
     }
     void Destroy()
     {

@@ -38,7 +38,7 @@ def _lib():
         L.kr_ops_last_error.restype = ctypes.c_char_p
         L.kr_ops_last_error.argtypes = []
         L.kr_op_gemm.argtypes = [i32, vp, i64, vp, i64, vp, i64, vp, i32, i32, i32, i32,
-                                 ctypes.POINTER(KrPub), vp]
+                                 ctypes.POINTER(KrWait), ctypes.POINTER(KrPub), vp]
         L.kr_op_elementwise.argtypes = [i32, i32, i32, vp, vp, vp, i32, i32, i32, i32,
                                         ctypes.POINTER(KrWait), ctypes.POINTER(KrPub), vp]
         L.kr_op_rowop.argtypes = [i32, i32, vp, vp, vp, vp, vp, vp, i32, i32, f32, i32, i32,
@@ -49,6 +49,10 @@ def _lib():
         L.kr_op_rope.argtypes = [i32, vp, i64, i32, i32, i32, vp, vp, vp]
         L.kr_op_attention.argtypes = [i32, vp, i64, vp, i64, vp, i64, vp, i64, i32, i32, i32, i32, f32, vp]
         L.kr_op_transpose.argtypes = [vp, vp, i32, i32, vp]
+        L.kr_op_stream_create.argtypes = []
+        L.kr_op_stream_create.restype = vp
+        L.kr_op_stream_destroy.argtypes = [vp]
+        L.kr_op_stream_destroy.restype = ctypes.c_int
         for name in ("kr_op_gemm", "kr_op_elementwise", "kr_op_rowop", "kr_op_wait", "kr_op_publish",
                      "kr_op_embedding", "kr_op_rope", "kr_op_attention", "kr_op_transpose"):
             getattr(L, name).restype = ctypes.c_int
@@ -81,6 +85,23 @@ def _stream(stream):
     return ctypes.c_void_p(s.cuda_stream)
 
 
+class QueueStream:
+    """A stream on a hardware queue of its own (kr_op_stream_create): relay
+    parties that wait on each other on the device need two of these. Usable
+    wherever the op wrappers take a stream."""
+
+    def __init__(self):
+        h = _lib().kr_op_stream_create()
+        if not h:
+            raise RuntimeError("kr_op_stream_create failed: %s" % _lib().kr_ops_last_error().decode())
+        self.cuda_stream = h
+
+    def close(self):
+        if self.cuda_stream:
+            _check(_lib().kr_op_stream_destroy(ctypes.c_void_p(self.cuda_stream)))
+            self.cuda_stream = None
+
+
 def _check(rc):
     if rc != 0:
         raise RuntimeError("kernrelay op failed: %s" % _lib().kr_ops_last_error().decode())
@@ -95,13 +116,15 @@ def make_pub(ctrl, flag0, rows_per_tile):
     return KrPub(ctypes.c_void_p(ctrl.data_ptr()), flag0, rows_per_tile, 0)
 
 
-def gemm(A, Bt, C, bias=None, pub=None, bm=0, stream=None):
-    """C[M,N] = A[M,K] @ Bt[N,K]^T (+bias), bf16/f16 in and out."""
+def gemm(A, Bt, C, bias=None, pub=None, bm=0, wait=None, stream=None):
+    """C[M,N] = A[M,K] @ Bt[N,K]^T (+bias), bf16/f16 in and out. `wait`: each
+    workgroup first waits for the relay tiles of A it reads."""
     M, K = A.shape
     N = Bt.shape[0]
     assert Bt.shape[1] == K and C.shape[0] == M and C.shape[1] == N
     _check(_lib().kr_op_gemm(_dt(A), _ptr(A), A.stride(0), _ptr(Bt), Bt.stride(0), _ptr(C), C.stride(0),
-                             _ptr(bias), M, N, K, bm, ctypes.byref(pub) if pub else None, _stream(stream)))
+                             _ptr(bias), M, N, K, bm, ctypes.byref(wait) if wait else None,
+                             ctypes.byref(pub) if pub else None, _stream(stream)))
 
 
 def elementwise(op, x0, y, x1=None, rows=None, cols=None, tile_rows=0, grid=0, wait=None, pub=None,

@@ -248,23 +248,67 @@ def test_relay_gemm_to_consumer_bit_exact(gpu):
     ctrl = torch.zeros(k * ops.CTRL_WORDS, dtype=torch.int32, device="cuda")
     C = torch.empty_like(ref_c)
     Y = torch.empty_like(ref_c)
-    sp, sc = torch.cuda.Stream(), torch.cuda.Stream()
+    sp, sc = ops.QueueStream(), ops.QueueStream()
     runs = 3
-    for _ in range(runs):
-        C.zero_()
-        Y.zero_()
-        torch.cuda.synchronize()
-        w = ops.make_wait(ctrl, 0, 0, M // k, adv=(0, k))
-        # consumer launched first: it must wait for the producer's releases
-        ops.elementwise("gelu", C, Y, tile_rows=M // k, grid=32, wait=w, stream=sc)
-        ops.gemm(A, Bt, C, pub=ops.make_pub(ctrl, 0, M // k), stream=sp)
-        torch.cuda.synchronize()
-        assert torch.equal(C, ref_c)
-        assert torch.equal(Y, ref_y)
+    try:
+        for _ in range(runs):
+            C.zero_()
+            Y.zero_()
+            torch.cuda.synchronize()
+            w = ops.make_wait(ctrl, 0, 0, M // k, adv=(0, k))
+            # consumer launched first: it must wait for the producer's releases
+            ops.elementwise("gelu", C, Y, tile_rows=M // k, grid=32, wait=w, stream=sc)
+            ops.gemm(A, Bt, C, pub=ops.make_pub(ctrl, 0, M // k), stream=sp)
+            torch.cuda.synchronize()
+            assert torch.equal(C, ref_c)
+            assert torch.equal(Y, ref_y)
+    finally:
+        sp.close()
+        sc.close()
     blk = ctrl.cpu().reshape(k, ops.CTRL_WORDS)
     assert torch.all(blk[:, 0] == runs) and torch.all(blk[:, 1] == runs)   # published == consumed
     assert torch.all(blk[:, 2] == 1)                                        # status ok
     assert torch.all(blk[:, 3] == 0) and torch.all(blk[:, 4] == 0)          # tickets reset
+
+
+def test_relay_gemm_waits_on_consumer_tiles(gpu):
+    """The GEMM as a relay consumer: a GELU releases k row tiles on one
+    stream; a GEMM launched first on another stream waits, per workgroup, for
+    the tiles its rows of A come from. C equals GELU-then-GEMM run serially bit
+    for bit, and each tile is consumed exactly once per run with status 1."""
+    announce("relay gelu->gemm k=4 (fused gemm wait)")
+    M, N, K, k = 1024, 768, 512, 4
+    X = rand((M, K), 1.0, 26).cuda()
+    Bt = rand((N, K), 0.02, 27).cuda()
+    ref_a = torch.empty(M, K, dtype=torch.bfloat16, device="cuda")
+    ref_c = torch.empty(M, N, dtype=torch.bfloat16, device="cuda")
+    ops.elementwise("gelu", X, ref_a)
+    ops.gemm(ref_a, Bt, ref_c)
+    torch.cuda.synchronize()
+
+    ctrl = torch.zeros(k * ops.CTRL_WORDS, dtype=torch.int32, device="cuda")
+    A = torch.empty_like(ref_a)
+    C = torch.empty_like(ref_c)
+    sp, sc = ops.QueueStream(), ops.QueueStream()
+    runs = 3
+    try:
+        for _ in range(runs):
+            A.zero_()
+            C.zero_()
+            torch.cuda.synchronize()
+            w = ops.make_wait(ctrl, 0, 0, M // k, adv=(0, k))
+            ops.gemm(A, Bt, C, wait=w, stream=sc)
+            ops.elementwise("gelu", X, A, tile_rows=M // k, pub=ops.make_pub(ctrl, 0, M // k), stream=sp)
+            torch.cuda.synchronize()
+            assert torch.equal(A, ref_a)
+            assert torch.equal(C, ref_c)
+    finally:
+        sp.close()
+        sc.close()
+    blk = ctrl.cpu().reshape(k, ops.CTRL_WORDS)
+    assert torch.all(blk[:, 0] == runs) and torch.all(blk[:, 1] == runs)
+    assert torch.all(blk[:, 2] == 1)
+    assert torch.all(blk[:, 3] == 0) and torch.all(blk[:, 4] == 0)
 
 
 def test_relay_wait_bound_reports_timeout(gpu):
