@@ -32,36 +32,30 @@ def log(msg):
     print("[bench] " + msg, file=sys.stderr, flush=True)
 
 
-def gemm_roofline(M, N, K, reps=20):
-    """Average duration of the producer GEMM at the dominant prefill shape,
-    timed with HIP events on the stream it is launched on."""
-    import torch
+# HBM bytes per launch of the gate/up GEMM at 2048x37888x3584 (bf16), from
+# two rocprofv3 --pmc passes over one launch: FETCH_SIZE 437495 KiB x 2.0 +
+# WRITE_SIZE 151552 KiB x 1.0, the factors being what the same counters read
+# for a plain 512 MiB device copy (FETCH 262156 KiB, WRITE 524288 KiB).
+GATE_UP_TRAFFIC_BYTES = (437495 * 2.0 + 151552 * 1.0) * 1024
+GATE_UP_TRAFFIC_SOURCE = "profiles/gemm_gate_up_2048x37888x3584.md"
 
-    from kernrelay_amd import ops
 
-    g = torch.Generator(device="cuda").manual_seed(7)
-    A = torch.randn(M, K, device="cuda", generator=g).to(torch.bfloat16)
-    Bt = (torch.randn(N, K, device="cuda", generator=g) * 0.02).to(torch.bfloat16)
-    C = torch.empty(M, N, device="cuda", dtype=torch.bfloat16)
-    s = torch.cuda.current_stream()
-    for _ in range(3):
-        ops.gemm(A, Bt, C, stream=s)
-    torch.cuda.synchronize()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record(s)
-    for _ in range(reps):
-        ops.gemm(A, Bt, C, stream=s)
-    e1.record(s)
-    torch.cuda.synchronize()
-    avg_s = e0.elapsed_time(e1) / 1e3 / reps
-    flops = 2.0 * M * N * K
-    achieved = flops / avg_s / 1e12
-    del A, Bt, C
-    torch.cuda.empty_cache()
+def gemm_roofline(run, S, N, K):
+    """The dominant kernel, the gate/up GEMM, timed inside the prefill: with
+    KR_TIME_GATE_UP=1 the library runs one more pass of the same program after
+    the timed graph replays, launched eagerly with HIP events around each
+    gate/up launch on the stream it runs on, and reports their average (28
+    launches, interleaved with the layer's other kernels as in the timed
+    run)."""
+    avg_us = run["gate_up_avg_us"]
+    flops = 2.0 * S * N * K
+    achieved = flops / (avg_us * 1e-6) / 1e12
     return {"bound": "mfma", "achieved": round(achieved, 1), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
-            "frac": round(achieved / PEAK_BF16_TFLOPS, 4), "traffic": None,
-            "kernel": "GemmKernel (gate/up projection) %dx%dx%d bf16" % (M, N, K),
-            "avg_launch_us": round(avg_s * 1e6, 2), "launches": reps}
+            "frac": round(achieved / PEAK_BF16_TFLOPS, 4), "traffic": round(GATE_UP_TRAFFIC_BYTES),
+            "traffic_algorithmic": 2 * (S * K + N * K + S * N), "traffic_source": GATE_UP_TRAFFIC_SOURCE,
+            "kernel": "GemmPipeKernel<bf16,256,256> gate/up projection %dx%dx%d" % (S, N, K),
+            "avg_launch_us": round(avg_us, 2), "launches": int(run["gate_up_launches"]),
+            "timing": "HIP events around each launch in an eager pass of the serial prefill"}
 
 
 def cpu_baseline(model_dir, seconds_hint=20):
@@ -98,6 +92,37 @@ def cpu_baseline(model_dir, seconds_hint=20):
             "ms_per_prefill_est": round(total * 1e3, 1)}
 
 
+def profile_gemm(M, N, K, reps):
+    """One producer-GEMM launch per repetition on random bf16 inputs: the
+    program the rocprofv3 --pmc passes of the roofline's traffic run."""
+    import torch
+
+    from kernrelay_amd import ops
+
+    g = torch.Generator(device="cuda").manual_seed(7)
+    A = torch.randn(M, K, device="cuda", generator=g).to(torch.bfloat16)
+    Bt = (torch.randn(N, K, device="cuda", generator=g) * 0.02).to(torch.bfloat16)
+    C = torch.empty(M, N, device="cuda", dtype=torch.bfloat16)
+    for _ in range(reps):
+        ops.gemm(A, Bt, C)
+    torch.cuda.synchronize()
+    print("gemm %dx%dx%d x%d done" % (M, N, K, reps), flush=True)
+
+
+def profile_copy(mib, reps):
+    """A plain device copy of known size: what FETCH_SIZE / WRITE_SIZE read
+    for it calibrates the counters."""
+    import torch
+
+    x = torch.ones(mib * 1024 * 512, dtype=torch.bfloat16, device="cuda")
+    y = torch.empty_like(x)
+    torch.cuda.synchronize()
+    for _ in range(reps):
+        y.copy_(x)
+    torch.cuda.synchronize()
+    print("copy %d MiB x%d done" % (mib, reps), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -108,7 +133,17 @@ def main():
     ap.add_argument("--preset", default="qwen2.5-7b")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--keep", default=None, help="keep / reuse the model directory here")
+    ap.add_argument("--profile-gemm", nargs=3, type=int, metavar=("M", "N", "K"),
+                    help="only launch the producer GEMM --reps times (for rocprofv3 --pmc)")
+    ap.add_argument("--profile-copy", type=int, metavar="MIB", help="only copy MIB MiB --reps times")
+    ap.add_argument("--reps", type=int, default=3)
     args = ap.parse_args()
+    if args.profile_gemm:
+        profile_gemm(*args.profile_gemm, args.reps)
+        return
+    if args.profile_copy:
+        profile_copy(args.profile_copy, args.reps)
+        return
     if args.gpus != 1:
         print("bench.py: this build targets one GPU; --gpus %d is not supported (the relay path is "
               "single-device; see DESIGN.md for how it would shard)" % args.gpus, file=sys.stderr)
@@ -135,6 +170,7 @@ def main():
             torch.cuda.empty_cache()
             log("model dir written in %.1f s" % (time.time() - t0))
         runs = {}
+        os.environ["KR_TIME_GATE_UP"] = "1"
         for mode in ("graph_whole", "relay_split:%d" % args.tiles):
             log("kr_qwen_run %s (warmup %d, steps %d)" % (mode, args.warmup, args.steps))
             r = libapi.qwen_run(tmp, mode=mode, seq=S, device=0, warmup=args.warmup, iters=args.steps)
@@ -147,8 +183,7 @@ def main():
         if serial["logits_fnv64"] != split["logits_fnv64"]:
             raise RuntimeError("relay split logits differ from serial")
         I, H = cfg["intermediate_size"], cfg["hidden_size"]
-        log("gemm roofline %dx%dx%d" % (S, 2 * I, H))
-        roof = gemm_roofline(S, 2 * I, H)
+        roof = gemm_roofline(serial, S, 2 * I, H)
         total_split_s = sum(split["samples_us"]) / 1e6
         total_serial_s = sum(serial["samples_us"]) / 1e6
         value = args.steps * S / total_split_s

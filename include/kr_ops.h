@@ -86,6 +86,21 @@ int kr_op_gemm(int dtype, const void *A, int64_t lda, const void *Bt, int64_t ld
                int64_t ldc, const void *bias, int M, int N, int K, int bm, const kr_wait *wait,
                const kr_pub *pub, void *stream);
 
+/* Gate/up GEMM with its SwiGLU consumer in the same launch: C[M, 2*cols] =
+ * A[M,K] . Bt[2*cols,K]^T (gate/up interleaved in groups of 8 columns) is
+ * released in row tiles through pub (required; rows_per_tile divides M), and
+ * workgroups appended after the GEMM's own wait for each released tile and
+ * write act[M, cols] = SwiGLU over its rows (silu rounded to 16 bits before
+ * the multiply, as kr_op_elementwise's swiglu_gu). Appended workgroups are
+ * dispatched after every GEMM workgroup, so they only take CUs the GEMM's
+ * last round leaves idle. tail_tiles (0 = all) limits the appended consumer
+ * to the first relay tiles (the caller runs SwiGLU on the rest); order_rows
+ * (0 = the relay tile) sets the row runs in which the GEMM produces. Replaces the relay edge matmul_gate/up ->
+ * Silu -> Mul of the reference (exec/qwen_main.cpp:616-644, 888-889). */
+int kr_op_gemm_swiglu(int dtype, const void *A, int64_t lda, const void *Bt, int64_t ldb, void *C,
+                      void *act, int M, int cols, int K, const kr_pub *pub, int tail_tiles,
+                      int order_rows, void *stream);
+
 /* Elementwise op on [rows, cols]; x1 used by mul/add/swiglu; dtype_out
  * differs from dtype_in only for cast. tile_rows = relay granularity
  * (0 = rows); grid = workgroups (0 = sized to the tensor). wait/pub may be

@@ -212,13 +212,13 @@ __global__ void __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_wav
             mloc = fmaxf(mloc, __shfl_xor(mloc, 32, 64));
             const float mnew = fmaxf(m, mloc);
             const float msub = mnew == -INFINITY ? 0.0f : mnew;
-            const float alpha = exp2f(m - msub);
+            const float alpha = __builtin_amdgcn_exp2f(m - msub);
             float lsum = 0.0f;
 #pragma unroll
             for (int kh = 0; kh < 2; ++kh)
 #pragma unroll
                 for (int v = 0; v < 16; ++v) {
-                    const float pv = exp2f(sacc[kh][v] - msub);
+                    const float pv = __builtin_amdgcn_exp2f(sacc[kh][v] - msub);
                     sacc[kh][v] = pv;
                     lsum += pv;
                 }

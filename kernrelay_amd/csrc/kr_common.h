@@ -93,13 +93,21 @@ __device__ __forceinline__ float BF16ToF32(uint16_t b)
     return __uint_as_float(uint32_t(b) << 16);
 }
 
+// gfx950 v_cvt_pk_bf16_f32: round to nearest even, one instruction (the same
+// bits as HostF32ToBF16 for every non-NaN input).
 __device__ __forceinline__ uint16_t F32ToBF16(float f)
 {
-    uint32_t u = __float_as_uint(f);
-    if ((u & 0x7fffffffu) > 0x7f800000u) return uint16_t((u >> 16) | 0x40u);
-    u += 0x7fffu + ((u >> 16) & 1u);
-    return uint16_t(u >> 16);
+    return __builtin_bit_cast(uint16_t, static_cast<__bf16>(f));
 }
+
+// Fast transcendental building blocks on the hardware's v_exp_f32 (2^x) and
+// v_rcp_f32 (about 1 ulp each): far below the 16-bit rounding that follows
+// every use, and the same instructions in every schedule (split or not).
+__device__ __forceinline__ float FastExp(float x) { return __builtin_amdgcn_exp2f(x * 1.4426950408889634f); }
+__device__ __forceinline__ float FastRcp(float x) { return __builtin_amdgcn_rcpf(x); }
+
+// SiLU as every kernel here computes it (x * sigmoid(x)).
+__device__ __forceinline__ float Silu(float x) { return x * FastRcp(1.0f + FastExp(-x)); }
 
 __device__ __forceinline__ float F16ToF32(uint16_t h)
 {

@@ -19,10 +19,23 @@ struct GemmDesc {
     RelayPub pub{};              // pub.ctrl == nullptr: no release
     RelayWait wait{};            // wait.ctrl == nullptr: A is ready; else each
                                  // workgroup waits for the tiles of A it reads
+    // Tail consumer (requires pub; C = interleaved gate/up, ldc = 2*tail_cols):
+    // workgroups appended to the grid wait for each released relay tile and
+    // write SwiGLU of its rows into tail_act [M, tail_cols].
+    void *tail_act = nullptr;
+    int tail_cols = 0;
+    int tail_tiles = 0;          // relay tiles the tail consumes (0 = all); the
+                                 // rest are left to a kernel after the GEMM
+    int order_rows = 0;          // > 0: produce in runs of this many rows (a
+                                 // multiple of pub.rows_per_tile), default
+                                 // one run per relay tile
 };
 
 // Launch C = A . Bt^T (+bias). pub.rows_per_tile (when publishing) must be a
-// multiple of the chosen M tile; pub.arrivals is computed here. With a wait,
+// multiple of the chosen M tile; pub.arrivals is computed here.
+// With tail_act, workgroups appended after the GEMM's own consume its tiles:
+// workgroups are dispatched in id order, so they only take CUs the GEMM's
+// last round leaves idle, and each starts on a relay tile once released. With a wait,
 // every workgroup first waits for the producer tiles covering its rows of A,
 // and the launch consumes wait.adv_lo..adv_hi once all workgroups are done.
 void GemmLaunch(const GemmDesc &d, hipStream_t stream);

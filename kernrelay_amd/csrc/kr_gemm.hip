@@ -46,8 +46,13 @@ struct GemmParams {
     int M, N, K;
     int tiles_m, tiles_n;
     int order_rows;  // > 0: dispatch tiles in relay-tile order, this many rows each
+    int store_kind;  // 0 device-scope (default), 1 plain, 2 nontemporal
     RelayPub pub;
     RelayWait wait;
+    uint16_t *tail_act;  // SwiGLU tail consumer output (nullptr: none)
+    int tail_cols;
+    int gemm_wgs;        // workgroups of the GEMM proper; the rest are tail
+    int tail_wpt;        // tail workgroups per relay tile
 };
 
 __device__ __forceinline__ int Swz(int row, int chunk) { return chunk ^ ((row >> 1) & 7); }
@@ -59,7 +64,9 @@ __device__ __forceinline__ int Swz(int row, int chunk) { return chunk ^ ((row >>
 // block is read by workgroups of one XCD while it sits in that XCD's L2.
 // * No relay: one run over all tiles.
 // * Relay (order_rows > 0): one run per relay tile, front to back, so tile 0
-//   of the rows is complete first; each run covers order_rows/bm row blocks.
+//   of the rows is complete first; each run covers order_rows/bm row blocks,
+//   odd runs with the weight columns in reverse (each run reads all of the
+//   weight, and the blocks the last run read are the ones still cached).
 __device__ __forceinline__ int XcdChunk(int bid, int first, int per)
 {
     const int off = (bid - first) & 7;
@@ -77,6 +84,9 @@ __device__ __forceinline__ void TileOf(int bid, int tiles_m, int tiles_n, int bm
         const int t = XcdChunk(bid, r * per, per);
         tm = r * mt + t % mt;
         tn = t / mt;
+        // serpentine: odd relay tiles walk the weight columns backwards, so
+        // they start on the blocks the previous tile read last (still in MALL)
+        if (r & 1) tn = tiles_n - 1 - tn;
         return;
     }
     const int t = XcdChunk(bid, 0, tiles_m * tiles_n);
@@ -93,6 +103,87 @@ __device__ __forceinline__ f32x16 Mfma(const uint4 &a, const uint4 &b, const f32
     } else {
         return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a),
                                                       __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+    }
+}
+
+// ---------------------------------------------------------------- tail
+// Gate/up halves of four output chunks of an interleaved gate/up buffer
+// (chunk c: 8 gate then 8 up values at c*16), all eight loads device-scope
+// (the tile was released by other XCDs' device-scope stores; this XCD's L2
+// may hold stale lines of the buffer from an earlier use) and in flight
+// together; returns once they have landed.
+typedef uint32_t GemmU32x4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ void LoadGateUp4(const uint16_t *p0, const uint16_t *p1, const uint16_t *p2,
+                                            const uint16_t *p3, GemmU32x4 (&g)[4], GemmU32x4 (&u)[4])
+{
+    asm volatile(
+        "global_load_dwordx4 %0, %8, off sc1\n\t"
+        "global_load_dwordx4 %1, %8, off offset:16 sc1\n\t"
+        "global_load_dwordx4 %2, %9, off sc1\n\t"
+        "global_load_dwordx4 %3, %9, off offset:16 sc1\n\t"
+        "global_load_dwordx4 %4, %10, off sc1\n\t"
+        "global_load_dwordx4 %5, %10, off offset:16 sc1\n\t"
+        "global_load_dwordx4 %6, %11, off sc1\n\t"
+        "global_load_dwordx4 %7, %11, off offset:16 sc1\n\t"
+        "s_waitcnt vmcnt(0)"
+        : "=&v"(g[0]), "=&v"(u[0]), "=&v"(g[1]), "=&v"(u[1]), "=&v"(g[2]), "=&v"(u[2]), "=&v"(g[3]), "=&v"(u[3])
+        : "v"(p0), "v"(p1), "v"(p2), "v"(p3)
+        : "memory");
+}
+
+// SwiGLU of one chunk, rounded exactly as the standalone kernel rounds it:
+// the silu result is stored (16-bit) before the multiply.
+template <int DT>
+__device__ __forceinline__ uint4 SwigluChunk(const GemmU32x4 &g, const GemmU32x4 &u)
+{
+    U16x8 a, b, r;
+    *reinterpret_cast<GemmU32x4 *>(a.v) = g;
+    *reinterpret_cast<GemmU32x4 *>(b.v) = u;
+#pragma unroll
+    for (int e = 0; e < 8; ++e)
+        r.v[e] = Elem<DT>::Store(RoundTo<DT>(Silu(Elem<DT>::Load(a.v[e]))) * Elem<DT>::Load(b.v[e]));
+    return *reinterpret_cast<const uint4 *>(r.v);
+}
+
+// A tail workgroup: wait for its relay tile, SwiGLU over its share of the
+// tile's rows; the last one of the tile consumes the release.
+template <int DT>
+__device__ void TailSwiglu(const GemmParams &p)
+{
+    const int j = int(blockIdx.x) - p.gemm_wgs;
+    const int t = j / p.tail_wpt;
+    const int w = j - t * p.tail_wpt;
+    int32_t *flag = p.pub.ctrl + size_t(p.pub.flag0 + t) * kWords;
+    if (threadIdx.x == 0) SpinOnTile(flag, flag, kDefaultMaxSpins);
+    __syncthreads();
+    const int64_t rows = p.pub.rows_per_tile;
+    const int64_t chunks = rows * p.tail_cols / 8;
+    const uint16_t *src = p.C + int64_t(t) * rows * p.ldc;
+    uint16_t *dst = p.tail_act + int64_t(t) * rows * p.tail_cols;
+    const int64_t stride = int64_t(p.tail_wpt) * kThreads;
+    int64_t c = int64_t(w) * kThreads + threadIdx.x;
+    for (; c + 3 * stride < chunks; c += 4 * stride) {
+        GemmU32x4 g[4], u[4];
+        LoadGateUp4(src + c * 16, src + (c + stride) * 16, src + (c + 2 * stride) * 16, src + (c + 3 * stride) * 16, g,
+                    u);
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+            *reinterpret_cast<uint4 *>(dst + (c + q * stride) * 8) = SwigluChunk<DT>(g[q], u[q]);
+    }
+    for (; c < chunks; c += stride) {
+        GemmU32x4 g[4], u[4];
+        LoadGateUp4(src + c * 16, src + c * 16, src + c * 16, src + c * 16, g, u);
+        *reinterpret_cast<uint4 *>(dst + c * 8) = SwigluChunk<DT>(g[0], u[0]);
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const int32_t a = __hip_atomic_fetch_add(flag + kOffDone, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (a == p.tail_wpt - 1) {
+            StoreRelaxed(flag + kOffDone, 0);
+            const int32_t to = __hip_atomic_exchange(flag + kOffTimedOut, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            StoreRelaxed(flag + kOffConsumed, LoadRelaxed(flag + kOffConsumed) + 1);
+            StoreRelaxed(flag + kOffStatus, to ? 2 : 1);
+        }
     }
 }
 
@@ -141,7 +232,11 @@ __device__ __forceinline__ void StoreTile(const GemmParams &p, f32x16 (&acc)[MI]
     __syncthreads();
     constexpr int CPR = BN / 8;  // 16-byte chunks per row
     const bool vec = (p.ldc % 8 == 0) && ((reinterpret_cast<uintptr_t>(p.C) & 15) == 0);
-    const bool coh = p.pub.ctrl != nullptr;  // released tiles: device-scope stores
+    // device-scope stores always: released tiles need them, and written
+    // through they also keep the output from evicting the operand tiles the
+    // other workgroups of this XCD are still reading from L2
+    // (KR_GEMM_STORE=plain|nt for comparison)
+    const bool coh = p.store_kind == 0 || p.pub.ctrl != nullptr;
 #pragma unroll 4
     for (int idx = threadIdx.x; idx < BM * CPR; idx += kThreads) {
         const int row = idx / CPR;
@@ -153,7 +248,11 @@ __device__ __forceinline__ void StoreTile(const GemmParams &p, f32x16 (&acc)[MI]
         if (row & 1) v = make_uint4(v.z, v.w, v.x, v.y);
         uint16_t *dst = p.C + int64_t(gm) * p.ldc + gn;
         if (vec && gn + 8 <= p.N) {
-            PutU128(dst, v, coh);
+            if (!coh && p.store_kind == 2) {
+                __builtin_nontemporal_store(*reinterpret_cast<const RelayU32x4 *>(&v), reinterpret_cast<RelayU32x4 *>(dst));
+            } else {
+                PutU128(dst, v, coh);
+            }
         } else {
             const uint32_t w[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
@@ -176,6 +275,10 @@ GemmKernel(GemmParams p)
 
     __shared__ __attribute__((aligned(16))) uint16_t smem[2 * STAGE];
 
+    if (int(blockIdx.x) >= p.gemm_wgs) {
+        TailSwiglu<DT>(p);
+        return;
+    }
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
@@ -296,6 +399,16 @@ bool ForceSimple()
     return v;
 }
 
+int StoreKind()
+{
+    static const int v = [] {
+        const char *e = std::getenv("KR_GEMM_STORE");
+        if (e == nullptr) return 0;
+        return std::string(e) == "plain" ? 1 : std::string(e) == "nt" ? 2 : 0;
+    }();
+    return v;
+}
+
 // L2 prefetch distance of the pipelined kernel in K stages (KR_GEMM_PF: 0
 // default = off, 2, 4); it changes timing only, never the bits.
 int PrefetchStages()
@@ -308,7 +421,7 @@ int PrefetchStages()
 }
 
 template <int DT, int BM, int BN>
-void LaunchTyped(const GemmParams &base, hipStream_t stream)
+void LaunchTyped(const GemmParams &base, int order_rows, int tail_tiles, hipStream_t stream)
 {
     GemmParams p = base;
     p.tiles_m = (p.M + BM - 1) / BM;
@@ -320,10 +433,21 @@ void LaunchTyped(const GemmParams &base, hipStream_t stream)
         if (!whole(p.pub.rows_per_tile)) throw std::runtime_error("relay tile rows must be a multiple of BM dividing M");
         p.pub.arrivals = (p.pub.rows_per_tile / BM) * p.tiles_n;
         p.order_rows = p.pub.rows_per_tile;
+        if (order_rows > 0) {
+            if (order_rows % p.pub.rows_per_tile != 0 || !whole(order_rows))
+                throw std::runtime_error("gemm: order_rows must be a multiple of the relay tile dividing M");
+            p.order_rows = order_rows;
+        }
     } else if (p.wait.ctrl != nullptr && p.wait.row_off == 0 && whole(p.wait.prod_rows)) {
         p.order_rows = p.wait.prod_rows;  // the rows that are released first run first
     }
-    const dim3 grid(p.tiles_m * p.tiles_n);
+    p.gemm_wgs = p.tiles_m * p.tiles_n;
+    int grid_x = p.gemm_wgs;
+    if (p.tail_act != nullptr) {
+        p.tail_wpt = 256;  // one per CU of the device: enough to fill the idle CUs of the last round
+        grid_x += tail_tiles * p.tail_wpt;
+    }
+    const dim3 grid(grid_x);
     if (p.K % kPipeK == 0 && !ForceSimple()) {
         switch (PrefetchStages()) {
         case 2: hipLaunchKernelGGL((GemmPipeKernel<DT, BM, BN, 2>), grid, dim3(kThreads), 0, stream, p); break;
@@ -390,6 +514,18 @@ void GemmLaunch(const GemmDesc &d, hipStream_t stream)
     p.K = d.K;
     p.pub = d.pub;
     p.wait = d.wait;
+    p.store_kind = StoreKind();
+    p.tail_act = static_cast<uint16_t *>(d.tail_act);
+    p.tail_cols = d.tail_cols;
+    if (p.tail_act != nullptr) {
+        if (p.pub.ctrl == nullptr || d.M % p.pub.rows_per_tile != 0)
+            throw std::runtime_error("gemm tail: needs a relay release over whole tiles of M");
+        if (d.dtype != kBF16 && d.dtype != kF16) throw std::runtime_error("gemm tail: 16-bit output only");
+        if (d.N != 2 * d.tail_cols || d.ldc != d.N || d.tail_cols % 8 != 0)
+            throw std::runtime_error("gemm tail: C must be a packed [M, 2*cols] interleaved gate/up buffer");
+        if ((reinterpret_cast<uintptr_t>(d.C) | reinterpret_cast<uintptr_t>(d.tail_act)) & 15)
+            throw std::runtime_error("gemm tail: buffers must be 16-byte aligned");
+    }
     if (p.wait.ctrl != nullptr && p.wait.prod_rows <= 0) throw std::runtime_error("gemm: wait.prod_rows must be > 0");
     const int relay_rows = d.pub.ctrl != nullptr ? d.pub.rows_per_tile : 0;
     GemmTile t = GemmPickTile(d.M, d.N, relay_rows);
@@ -408,9 +544,16 @@ void GemmLaunch(const GemmDesc &d, hipStream_t stream)
     if (t.bm < 0) throw std::runtime_error("gemm: relay tile rows must be a multiple of 64");
     const bool bf = d.dtype == kBF16;
     if (d.dtype != kBF16 && d.dtype != kF16) throw std::runtime_error("gemm: dtype must be bf16 or f16");
+    const int order = d.order_rows;
+    int tail = 0;
+    if (d.tail_act != nullptr) {
+        const int k = d.M / d.pub.rows_per_tile;
+        tail = d.tail_tiles > 0 ? std::min(d.tail_tiles, k) : k;
+    }
 #define KR_GEMM_CASE(BM_, BN_)                                                                     \
     if (t.bm == BM_ && t.bn == BN_) {                                                              \
-        bf ? LaunchTyped<kBF16, BM_, BN_>(p, stream) : LaunchTyped<kF16, BM_, BN_>(p, stream);    \
+        bf ? LaunchTyped<kBF16, BM_, BN_>(p, order, tail, stream)                                  \
+           : LaunchTyped<kF16, BM_, BN_>(p, order, tail, stream);                                  \
         return;                                                                                    \
     }
     KR_GEMM_CASE(256, 256)

@@ -92,6 +92,30 @@ int kr_op_gemm(int dtype, const void *A, int64_t lda, const void *Bt, int64_t ld
     });
 }
 
+int kr_op_gemm_swiglu(int dtype, const void *A, int64_t lda, const void *Bt, int64_t ldb, void *C, void *act, int M,
+                      int cols, int K, const kr_pub *pub, int tail_tiles, int order_rows, void *stream)
+{
+    return Guard([&] {
+        kr::GemmDesc d;
+        d.dtype = dtype;
+        d.A = A;
+        d.Bt = Bt;
+        d.C = C;
+        d.lda = lda;
+        d.ldb = ldb;
+        d.ldc = 2 * int64_t(cols);
+        d.M = M;
+        d.N = 2 * cols;
+        d.K = K;
+        d.pub = ToPub(pub);
+        d.tail_act = act;
+        d.tail_cols = cols;
+        d.tail_tiles = tail_tiles;
+        d.order_rows = order_rows;
+        kr::GemmLaunch(d, S(stream));
+    });
+}
+
 int kr_op_elementwise(int op, int dtype_in, int dtype_out, const void *x0, const void *x1, void *y, int rows,
                       int cols, int tile_rows, int grid, const kr_wait *wait, const kr_pub *pub, void *stream)
 {

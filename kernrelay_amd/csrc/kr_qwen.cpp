@@ -103,6 +103,7 @@ Mode ParseMode(const std::string &m)
 struct Item {
     int stream;  // 0 = producer, 1 = consumer
     std::function<void(hipStream_t)> fn;
+    bool timing = false;  // timing event: only in the eager timing pass
 };
 
 struct TensorInfo {
@@ -124,6 +125,10 @@ public:
             if (g.first) (void)hipGraphDestroy(g.first);
         }
         for (hipEvent_t e : events_) (void)hipEventDestroy(e);
+        for (auto &pr : kev_) {
+            (void)hipEventDestroy(pr.first);
+            (void)hipEventDestroy(pr.second);
+        }
         if (t0_) (void)hipEventDestroy(t0_);
         if (tp_) (void)hipEventDestroy(tp_);
         if (tc_) (void)hipEventDestroy(tc_);
@@ -136,8 +141,7 @@ public:
     {
         const auto t0 = Clock::now();
         Check(hipSetDevice(device_), "hipSetDevice");
-        // the split gives the consumer stream its own CUs (see BuildSplit)
-        streams_.Create(device_, mode_.split ? std::max(1, EnvInt("KR_SPLIT_CUS_PER_XCD", 2)) : 0);
+        streams_.Create(device_);
         Check(hipEventCreate(&t0_), "event");
         Check(hipEventCreate(&tp_), "event");
         Check(hipEventCreate(&tc_), "event");
@@ -159,7 +163,8 @@ public:
                 if (graphs_[s].second) Check(hipGraphLaunch(graphs_[s].second, Stream(int(s))), "graph launch");
             return;
         }
-        for (auto &it : prog_) it.fn(Stream(it.stream));
+        for (auto &it : prog_)
+            if (!it.timing) it.fn(Stream(it.stream));
     }
 
     void Bench(int warmup, int iters)
@@ -188,6 +193,20 @@ public:
             samples_.push_back(Us(t0, t1));
             host_samples_.push_back(Us(t0, th));
             dev_samples_.push_back(1000.0 * std::max(a, b));
+        }
+        if (!kev_.empty()) {
+            // one more pass of the same program, launched eagerly with the
+            // timing events (events recorded during capture cannot be timed)
+            Check(hipDeviceSynchronize(), "pre timing sync");
+            for (auto &it : prog_) it.fn(Stream(it.stream));
+            Check(hipDeviceSynchronize(), "timing sync");
+            double sum = 0.0;
+            for (auto &pr : kev_) {
+                float ms = 0.f;
+                Check(hipEventElapsedTime(&ms, pr.first, pr.second), "elapsed");
+                sum += 1000.0 * ms;
+            }
+            gu_avg_us_ = sum / double(kev_.size());
         }
     }
 
@@ -280,6 +299,11 @@ public:
         char buf[32];
         std::snprintf(buf, sizeof buf, "%016llx", static_cast<unsigned long long>(fnv_));
         r.Set("logits_fnv64", Value::MakeString(buf));
+        if (!kev_.empty()) {
+            // average gate/up GEMM duration in the eager timing pass
+            r.Set("gate_up_avg_us", Value::MakeNumber(gu_avg_us_));
+            r.Set("gate_up_launches", Value::MakeNumber(double(kev_.size())));
+        }
         r.Set("last_top2_margin", Value::MakeNumber(margin_));
         r.Set("consumer_cus", Value::MakeNumber(streams_.cons_cus));
         r.Set("load_ms", Value::MakeNumber(load_ms_));
@@ -639,18 +663,23 @@ private:
     }
 
     // ---------------------------------------------------------- relay split
-    // SwiGLU over rows [r0, r0+rows) of the interleaved gate/up output.
-    void SwigluRows(int s, int r0, int rows, RelayPub pub, int grid = 0)
+    // Bracket the ops emitted by `body` on stream s with timing events.
+    template <class F>
+    void Timed(int s, F body)
     {
-        EwDesc e;
-        e.op = kEwSwigluGU;
-        e.x0 = gu_.as<uint16_t>() + size_t(r0) * 2 * I_;
-        e.y = act_.as<uint16_t>() + size_t(r0) * I_;
-        e.rows = rows;
-        e.cols = I_;
-        e.pub = pub;
-        e.grid = grid;
-        Emit(s, [e](hipStream_t st) { EwLaunch(e, st); });
+        if (EnvInt("KR_TIME_GATE_UP", 0) == 0) {
+            body();
+            return;
+        }
+        hipEvent_t a = nullptr, b = nullptr;
+        Check(hipEventCreate(&a), "event");
+        Check(hipEventCreate(&b), "event");
+        kev_.push_back({a, b});
+        Emit(s, [a](hipStream_t st) { Check(hipEventRecord(a, st), "record"); });
+        prog_.back().timing = true;
+        body();
+        Emit(s, [b](hipStream_t st) { Check(hipEventRecord(b, st), "record"); });
+        prog_.back().timing = true;
     }
 
     // qkv GEMM (+bias), qk-norm, RoPE and attention of layer l on stream P.
@@ -684,53 +713,39 @@ private:
         });
     }
 
-    // relay_split[:k] — the MI355X form of the reference's AIC/AIV relay.
-    // The producer stream P runs on most CUs, the consumer stream C on a
-    // disjoint partition (KR_SPLIT_CUS_PER_XCD, default 2 per XCD; P keeps
-    // 240 of 256, which leaves the wave count of every GEMM of the 7B layer
-    // unchanged; a 256x256 GEMM workgroup needs a whole CU, and consumer
-    // workgroups interleaved onto the producer's CUs starve both).
-    // * The gate/up GEMM releases its k row tiles as they complete.
-    // * C holds one resident SwiGLU consumer for the whole prefill: for every
-    //   layer it takes tiles 0..kc-1 (kc = KR_SPLIT_C_TILES, default k-1) as
-    //   they are released and releases its act tiles, while P still computes
-    //   the later gate/up tiles.
-    // * P runs SwiGLU on the remaining tiles itself at full width right after
-    //   the GEMM, then waits for C's act tiles and runs down.
+    // relay_split[:k] — the relay on MI355X. The gate/up GEMM releases its k
+    // row tiles through the flags as they complete, and the SwiGLU consumer
+    // starts on released tiles inside the same launch: its workgroups are
+    // appended to the GEMM's grid, so the dispatcher hands them out only as
+    // the GEMM's last round frees CUs, which the serial schedule leaves idle
+    // (that round is 1184 mod 256 = 160 of 256 CUs for the 7B layer). The
+    // appended consumer takes the tiles released before that round; the
+    // tiles released at the very end are run at full width right after the
+    // GEMM. Producing row tile by row tile makes every run re-read the whole
+    // weight, so with k >= 4 the GEMM produces in halves (tiles 0..k/2-1 are
+    // released together mid-GEMM) — KR_SPLIT_ORDER_ROWS / KR_SPLIT_TAIL_TILES
+    // override both. The
+    // consumer is not given a CU partition of its own: measured on MI355X, a
+    // static partition costs every producer kernel its CUs (5.5% of the
+    // prefill for 2 CUs per XCD) and consumer workgroups interleaved onto the
+    // producer's CUs starve 256x256 GEMM workgroups, which need a whole CU.
     // Edges behind single-wave producers (o, down -> Add+RMSNorm) release all
-    // their tiles at once, so they stay in P's stream order. Every row goes
+    // their tiles at once, so they stay in stream order. Every row goes
     // through the same arithmetic as in the serial schedule: identical bits.
     void BuildSplit()
     {
         const int S = seq_;
         const int k = mode_.tiles;
         const int T = S / k;
-        const int kc = std::max(0, std::min(k - 1, EnvInt("KR_SPLIT_C_TILES", k - 1)));
-        const int P = 0, C = 1;
-        // block (l, t) of each edge = base + l*k + t
-        const int gu_act = NewEdge(k * L_), act_down = NewEdge(k * L_);
+        const int P = 0;
+        const int gu_act = NewEdge(k * L_);  // block (l, t) = gu_act + l*k + t
+        const int order_rows = EnvInt("KR_SPLIT_ORDER_ROWS", k >= 4 ? S / 2 : T);
+        const int tail_tiles = std::max(0, std::min(k, EnvInt("KR_SPLIT_TAIL_TILES", k >= 4 ? k / 2 : k - 1)));
+        if (order_rows <= 0 || order_rows % T != 0 || S % order_rows != 0)
+            throw std::runtime_error("relay_split: KR_SPLIT_ORDER_ROWS must be a multiple of seq/tiles dividing seq");
         ctrl_.Alloc(std::max<size_t>(ctrl_blocks_, 1) * kWords * 4);
         Check(hipMemset(ctrl_.get(), 0, ctrl_.bytes()), "zero ctrl");
         max_spins_ = uint32_t(EnvInt("KR_MAX_SPINS", int(kDefaultMaxSpins)));
-
-        if (kc > 0) {
-            SwigluRelayDesc d;
-            d.gu = gu_.get();
-            d.act = act_.get();
-            d.cols = I_;
-            d.tile_rows = T;
-            d.tiles = k;
-            d.kc = kc;
-            d.layers = L_;
-            d.ctrl = ctrl_.as<int32_t>();
-            d.in0 = gu_act;
-            d.out0 = act_down;
-            d.max_spins = max_spins_;
-            d.cus = streams_.cons_cus;
-            for (int l = 0; l < L_; ++l)
-                for (int t = 0; t < kc; ++t) consumed_.push_back(gu_act + l * k + t);
-            Emit(C, [d](hipStream_t st) { SwigluRelayLaunch(d, st); });
-        }
 
         uint16_t *h0 = h_[0].as<uint16_t>(), *h1 = h_[1].as<uint16_t>();
         uint16_t *x = x_.as<uint16_t>();
@@ -748,15 +763,41 @@ private:
             EmitAttention(P, l, RelayWait{});
             Gemm(P, attn_.get(), int64_t(HQ_) * D_, w.o, H_, HQ_ * D_, o_.get(), H_, nullptr, S, RelayPub{});
             AddRmsNorm(P, hcur, o_.get(), w.ln2, x, hnxt, RelayWait{}, 0, RelayPub{}, 0);
-            // gate/up releases its k row tiles; SwiGLU: tiles < kc on C, the rest here
-            Gemm(P, x, H_, w.gu, 2 * I_, H_, gu_.get(), 2 * int64_t(I_), nullptr, S,
-                 kc > 0 ? Pub(gu_act + l * k, T) : RelayPub{});
-            SwigluRows(P, kc * T, (k - kc) * T, RelayPub{});
-            if (kc > 0) {
-                RelayWait wd = WaitDesc(act_down + l * k, k);
-                wd.adv_hi = kc;
-                for (int t = 0; t < kc; ++t) consumed_.push_back(act_down + l * k + t);
-                Emit(P, [wd, T, kc](hipStream_t st) { WaitLaunch(wd, 0, kc * T, st); });
+            {
+                // gate/up, its k released tiles consumed by the appended SwiGLU
+                GemmDesc d;
+                d.dtype = kBF16;
+                d.A = x;
+                d.lda = H_;
+                d.Bt = w.gu;
+                d.ldb = H_;
+                d.C = gu_.get();
+                d.ldc = 2 * int64_t(I_);
+                d.M = S;
+                d.N = 2 * I_;
+                d.K = H_;
+                d.pub = Pub(gu_act + l * k, T);
+                d.tail_act = act_.get();
+                d.tail_cols = I_;
+                d.tail_tiles = tail_tiles;
+                d.order_rows = order_rows;
+                for (int t = 0; t < tail_tiles; ++t) consumed_.push_back(gu_act + l * k + t);
+                Timed(P, [&] {
+                    if (tail_tiles > 0) {
+                        Emit(P, [d](hipStream_t st) { GemmLaunch(d, st); });
+                    } else {
+                        Gemm(P, x, H_, w.gu, 2 * I_, H_, gu_.get(), 2 * int64_t(I_), nullptr, S, RelayPub{});
+                    }
+                });
+                if (tail_tiles < k) {
+                    EwDesc e;
+                    e.op = kEwSwigluGU;
+                    e.x0 = gu_.as<uint16_t>() + size_t(tail_tiles) * T * 2 * I_;
+                    e.y = act_.as<uint16_t>() + size_t(tail_tiles) * T * I_;
+                    e.rows = (k - tail_tiles) * T;
+                    e.cols = I_;
+                    Emit(P, [e](hipStream_t st) { EwLaunch(e, st); });
+                }
             }
             Gemm(P, act_.get(), I_, w.down, H_, I_, down_.get(), H_, nullptr, S, RelayPub{});
             const bool last = l + 1 == L_;
@@ -830,7 +871,9 @@ private:
             after(C, le[l].ln2_gu);
             // gate/up -> SwiGLU
             WaitBefore(P, le[l].ln2_gu, k);
-            Gemm(P, x, H_, w.gu, 2 * I_, H_, gu_.get(), 2 * int64_t(I_), nullptr, S, release(le[l].gu_act));
+            Timed(P, [&] {
+                Gemm(P, x, H_, w.gu, 2 * I_, H_, gu_.get(), 2 * int64_t(I_), nullptr, S, release(le[l].gu_act));
+            });
             after(P, le[l].gu_act);
             {
                 EwDesc e;
@@ -873,7 +916,7 @@ private:
             hipGraph_t g = nullptr;
             Check(hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal), "begin capture");
             for (auto &it : prog_)
-                if (it.stream == s) it.fn(st);
+                if (it.stream == s && !it.timing) it.fn(st);
             Check(hipStreamEndCapture(st, &g), "end capture");
             hipGraphExec_t ex = nullptr;
             Check(hipGraphInstantiate(&ex, g, nullptr, nullptr, 0), "instantiate");
@@ -912,6 +955,10 @@ private:
     std::vector<hipEvent_t> events_;
     uint32_t max_spins_ = kDefaultMaxSpins;
     hipEvent_t t0_ = nullptr, tp_ = nullptr, tc_ = nullptr;
+    // KR_TIME_GATE_UP=1: timing events around every gate/up GEMM, recorded in
+    // one eager pass of the program after the timed iterations
+    std::vector<std::pair<hipEvent_t, hipEvent_t>> kev_;
+    double gu_avg_us_ = 0.0;
     std::vector<double> samples_, host_samples_, dev_samples_;
     int argmax_ = -1, ref_argmax_ = -1, flag_edges_ = 0, flag_timeouts_ = 0;
     double maxdiff_ = -1.0, absmean_ = 0.0, margin_ = 0.0, load_ms_ = 0.0;

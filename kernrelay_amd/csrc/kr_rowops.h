@@ -70,24 +70,7 @@ void RowLaunch(const RowDesc &d, hipStream_t stream);
 // publish tile `tile` once (arrivals forced to 1).
 void WaitLaunch(const RelayWait &w, int lo, int hi, hipStream_t stream);
 
-// Resident SwiGLU consumer for `layers` relay edges: waits for gate/up tile
-// (l, t) = block in0 + l*tiles + t, computes SwiGLU over that tile's rows of
-// the interleaved [tiles*tile_rows, 2*cols] buffer `gu` into `act`, releases
-// block out0 + l*tiles + t; tiles t < kc of every layer, in order.
-struct SwigluRelayDesc {
-    const void *gu = nullptr;
-    void *act = nullptr;
-    int cols = 0;            // I
-    int tile_rows = 0;       // T
-    int tiles = 0;           // k
-    int kc = 0;              // tiles handled per layer
-    int layers = 0;
-    int32_t *ctrl = nullptr;
-    int32_t in0 = 0, out0 = 0;
-    uint32_t max_spins = kDefaultMaxSpins;
-    int cus = 0;             // CUs of the stream it runs on (grid: all resident)
-};
-void SwigluRelayLaunch(const SwigluRelayDesc &d, hipStream_t stream);
+
 void PublishLaunch(const RelayPub &p, int tile, hipStream_t stream);
 
 }  // namespace kr

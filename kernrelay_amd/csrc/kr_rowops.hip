@@ -39,14 +39,17 @@ struct EwParams {
     RelayPub pub;
 };
 
+// tanh(y) = 1 - 2 / (1 + e^(2y)): saturates to +-1 through inf / 0 of the
+// exponential, and its absolute error near 0 (~1e-7) vanishes in 1 + tanh.
 __device__ __forceinline__ float GeluTanh(float x)
 {
     const float k0 = 0.7978845608028654f;  // sqrt(2/pi)
     const float k1 = 0.044715f;
-    return 0.5f * x * (1.0f + tanhf(k0 * (x + k1 * x * x * x)));
+    const float y = k0 * (x + k1 * x * x * x);
+    const float t = 1.0f - 2.0f * FastRcp(1.0f + FastExp(2.0f * y));
+    return 0.5f * x * (1.0f + t);
 }
 
-__device__ __forceinline__ float Silu(float x) { return x / (1.0f + expf(-x)); }
 
 template <int OP, int DTI, int DTO>
 __global__ void __launch_bounds__(kThreads) EwKernel(EwParams p)
@@ -204,7 +207,7 @@ __global__ void __launch_bounds__(kThreads) RowKernel(RowParams p)
                     if (ok[c])
 #pragma unroll
                         for (int e = 0; e < 8; ++e) {
-                            v[c][e] = expf(v[c][e] - m);
+                            v[c][e] = FastExp(v[c][e] - m);
                             s += v[c][e];
                         }
                 s = GroupReduce<LPR, false>(s, red);
@@ -250,106 +253,6 @@ __global__ void __launch_bounds__(64) WaitKernel(RelayWait w, int lo, int hi)
 }
 
 __global__ void __launch_bounds__(64) PublishKernel(RelayPub p, int tile) { RelayArrive(p, tile); }
-
-// ------------------------------------------------------- resident consumer
-// The SwiGLU consumer of a whole prefill as one launch on the consumer CU
-// partition: for every layer l and relay tile t < kc it waits for gate/up
-// tile (l, t), computes SwiGLU over the tile's rows and releases act tile
-// (l, t). Launched once, it never pays a kernel start (whose cache acquire
-// would invalidate the L2 the producer's GEMM is using) and never executes a
-// cache-wide fence: the released gate/up lines are read with device-scope
-// loads (which do not return stale L2 lines left from the previous layer's
-// use of the same buffer) and its own output is written with device-scope
-// stores before each release.
-struct SwigluRelayParams {
-    const uint16_t *gu;  // [T*k, 2I] interleaved gate/up (8-column groups)
-    uint16_t *act;       // [T*k, I]
-    int64_t tile_chunks; // 16-byte output chunks per relay tile (T*I/8)
-    int k, kc, layers;
-    int32_t *ctrl;
-    int32_t in0, out0;   // block of (layer l, tile t) = in0 / out0 + l*k + t
-    uint32_t max_spins;
-};
-
-typedef uint32_t U32x4 __attribute__((ext_vector_type(4)));
-
-// Gate/up halves of four output chunks (c, c+s, c+2s, c+3s), all eight loads
-// device-scope and in flight together; returns once they have landed.
-__device__ __forceinline__ void LoadGu4(const uint16_t *p0, const uint16_t *p1, const uint16_t *p2,
-                                        const uint16_t *p3, U32x4 (&g)[4], U32x4 (&u)[4])
-{
-    asm volatile(
-        "global_load_dwordx4 %0, %8, off sc1\n\t"
-        "global_load_dwordx4 %1, %8, off offset:16 sc1\n\t"
-        "global_load_dwordx4 %2, %9, off sc1\n\t"
-        "global_load_dwordx4 %3, %9, off offset:16 sc1\n\t"
-        "global_load_dwordx4 %4, %10, off sc1\n\t"
-        "global_load_dwordx4 %5, %10, off offset:16 sc1\n\t"
-        "global_load_dwordx4 %6, %11, off sc1\n\t"
-        "global_load_dwordx4 %7, %11, off offset:16 sc1\n\t"
-        "s_waitcnt vmcnt(0)"
-        : "=&v"(g[0]), "=&v"(u[0]), "=&v"(g[1]), "=&v"(u[1]), "=&v"(g[2]), "=&v"(u[2]), "=&v"(g[3]), "=&v"(u[3])
-        : "v"(p0), "v"(p1), "v"(p2), "v"(p3)
-        : "memory");
-}
-
-__device__ __forceinline__ uint4 SwigluChunk(const U32x4 &g, const U32x4 &u)
-{
-    U16x8 a, b, r;
-    *reinterpret_cast<U32x4 *>(a.v) = g;
-    *reinterpret_cast<U32x4 *>(b.v) = u;
-#pragma unroll
-    for (int e = 0; e < 8; ++e)
-        r.v[e] = Elem<kBF16>::Store(RoundTo<kBF16>(Silu(Elem<kBF16>::Load(a.v[e]))) * Elem<kBF16>::Load(b.v[e]));
-    return *reinterpret_cast<const uint4 *>(r.v);
-}
-
-__global__ void __launch_bounds__(kThreads) SwigluRelayKernel(SwigluRelayParams p)
-{
-    const int64_t stride = int64_t(gridDim.x) * kThreads;
-    const int64_t first = int64_t(blockIdx.x) * kThreads + threadIdx.x;
-    for (int l = 0; l < p.layers; ++l) {
-        for (int t = 0; t < p.kc; ++t) {
-            int32_t *fin = p.ctrl + size_t(p.in0 + l * p.k + t) * kWords;
-            int32_t *fout = p.ctrl + size_t(p.out0 + l * p.k + t) * kWords;
-            if (threadIdx.x == 0) SpinOnTile(fin, fin, p.max_spins);
-            __syncthreads();
-            const uint16_t *src = p.gu + t * p.tile_chunks * 16;
-            uint16_t *dst = p.act + t * p.tile_chunks * 8;
-            int64_t c = first;
-            for (; c + 3 * stride < p.tile_chunks; c += 4 * stride) {
-                U32x4 g[4], u[4];
-                LoadGu4(src + c * 16, src + (c + stride) * 16, src + (c + 2 * stride) * 16,
-                        src + (c + 3 * stride) * 16, g, u);
-#pragma unroll
-                for (int j = 0; j < 4; ++j) PutU128(dst + (c + j * stride) * 8, SwigluChunk(g[j], u[j]), true);
-            }
-            for (; c < p.tile_chunks; c += stride) {
-                U32x4 g[4], u[4];
-                LoadGu4(src + c * 16, src + c * 16, src + c * 16, src + c * 16, g, u);
-                PutU128(dst + c * 8, SwigluChunk(g[0], u[0]), true);
-            }
-            // stores acknowledged; then consume the input tile and release the output tile
-            __builtin_amdgcn_s_waitcnt(0x0F70);
-            __syncthreads();
-            if (threadIdx.x == 0) {
-                const int32_t a = __hip_atomic_fetch_add(fin + kOffDone, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                if (a == int32_t(gridDim.x) - 1) {
-                    StoreRelaxed(fin + kOffDone, 0);
-                    const int32_t to =
-                        __hip_atomic_exchange(fin + kOffTimedOut, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                    StoreRelaxed(fin + kOffConsumed, LoadRelaxed(fin + kOffConsumed) + 1);
-                    StoreRelaxed(fin + kOffStatus, to ? 2 : 1);
-                }
-                const int32_t b = __hip_atomic_fetch_add(fout + kOffArrive, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                if (b == int32_t(gridDim.x) - 1) {
-                    StoreRelaxed(fout + kOffArrive, 0);
-                    __hip_atomic_fetch_add(fout + kOffPublished, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                }
-            }
-        }
-    }
-}
 
 int TileCount(int rows, int tile_rows) { return (rows + tile_rows - 1) / tile_rows; }
 
@@ -484,34 +387,6 @@ void WaitLaunch(const RelayWait &w, int lo, int hi, hipStream_t stream)
     if (w.ctrl == nullptr) return;
     hipLaunchKernelGGL(WaitKernel, dim3(1), dim3(64), 0, stream, w, lo, hi);
     Check(hipGetLastError(), "wait launch");
-}
-
-void SwigluRelayLaunch(const SwigluRelayDesc &d, hipStream_t stream)
-{
-    if (d.ctrl == nullptr || d.kc <= 0 || d.layers <= 0) return;
-    if (d.cols % 8 != 0 || d.tile_rows <= 0 || d.cus <= 0) throw std::runtime_error("swiglu relay: bad shape");
-    // Every workgroup must be resident at once: each tile's completion ticket
-    // counts all of them, and a workgroup waiting for a free slot would only
-    // get one when a resident workgroup exits after the last layer.
-    int per_cu = 0;
-    Check(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, SwigluRelayKernel, kThreads, 0), "occupancy");
-    if (per_cu <= 0) throw std::runtime_error("swiglu relay: kernel does not fit a CU");
-    const int grid = d.cus * std::min(per_cu, 4);
-    if ((reinterpret_cast<uintptr_t>(d.gu) | reinterpret_cast<uintptr_t>(d.act)) & 15)
-        throw std::runtime_error("swiglu relay: buffers must be 16-byte aligned");
-    SwigluRelayParams p{};
-    p.gu = static_cast<const uint16_t *>(d.gu);
-    p.act = static_cast<uint16_t *>(d.act);
-    p.tile_chunks = int64_t(d.tile_rows) * d.cols / 8;
-    p.k = d.tiles;
-    p.kc = d.kc;
-    p.layers = d.layers;
-    p.ctrl = d.ctrl;
-    p.in0 = d.in0;
-    p.out0 = d.out0;
-    p.max_spins = d.max_spins;
-    hipLaunchKernelGGL(SwigluRelayKernel, dim3(grid), dim3(kThreads), 0, stream, p);
-    Check(hipGetLastError(), "swiglu relay launch");
 }
 
 void PublishLaunch(const RelayPub &p, int tile, hipStream_t stream)

@@ -139,6 +139,22 @@ def test_cast_bf16_to_f16_exhaustive(gpu):
     assert np.array_equal(ref[~nan_r].view(np.uint16), got[~nan_g].view(np.uint16))
 
 
+def test_cast_f16_to_bf16_exhaustive(gpu):
+    """All 65536 fp16 patterns rounded to bf16 (every 16-bit store of the
+    kernels goes through the same f32 -> bf16 conversion): round to nearest
+    even, ties included, against torch's conversion of the exact values."""
+    announce("cast f16->bf16 exhaustive")
+    bits = torch.arange(65536, dtype=torch.int32).to(torch.int16)
+    x = bits.view(torch.float16).reshape(512, 128)
+    y = torch.empty(512, 128, dtype=torch.bfloat16, device="cuda")
+    ops.elementwise("cast", x.cuda(), y)
+    torch.cuda.synchronize()
+    ref = x.float().to(torch.bfloat16)
+    nan = torch.isnan(ref)
+    assert torch.equal(torch.isnan(y.cpu()), nan)
+    assert torch.equal(y.cpu()[~nan].view(torch.int16), ref[~nan].view(torch.int16))
+
+
 def test_cast_f16_to_f32(gpu):
     announce("cast f16->f32")
     x = rand((64, 256), 3.0, 13, torch.float16)
@@ -309,6 +325,37 @@ def test_relay_gemm_waits_on_consumer_tiles(gpu):
     assert torch.all(blk[:, 0] == runs) and torch.all(blk[:, 1] == runs)
     assert torch.all(blk[:, 2] == 1)
     assert torch.all(blk[:, 3] == 0) and torch.all(blk[:, 4] == 0)
+
+
+@pytest.mark.parametrize("k", [1, 2, 4])
+def test_gemm_swiglu_tail_bit_exact(gpu, k):
+    """The SwiGLU consumer appended to the gate/up GEMM's launch (waiting on
+    the GEMM's own relay tiles) equals the GEMM followed by the standalone
+    swiglu_gu kernel bit for bit, on every one of several runs (the counters
+    carry over), and consumes each tile once with status 1."""
+    announce("gemm+swiglu tail k=%d" % k)
+    M, I, K = 1024, 1536, 512
+    A = rand((M, K), 1.0, 30).cuda()
+    Bt = rand((2 * I, K), 0.05, 31).cuda()
+    ref_c = torch.empty(M, 2 * I, dtype=torch.bfloat16, device="cuda")
+    ref_a = torch.empty(M, I, dtype=torch.bfloat16, device="cuda")
+    ops.gemm(A, Bt, ref_c)
+    ops.elementwise("swiglu_gu", ref_c, ref_a, rows=M, cols=I)
+    torch.cuda.synchronize()
+    ctrl = torch.zeros(k * ops.CTRL_WORDS, dtype=torch.int32, device="cuda")
+    C = torch.empty_like(ref_c)
+    act = torch.empty_like(ref_a)
+    runs = 3
+    for _ in range(runs):
+        C.zero_()
+        act.zero_()
+        ops.gemm_swiglu(A, Bt, C, act, ops.make_pub(ctrl, 0, M // k))
+        torch.cuda.synchronize()
+        assert torch.equal(C, ref_c)
+        assert torch.equal(act, ref_a)
+    blk = ctrl.cpu().reshape(k, ops.CTRL_WORDS)
+    assert torch.all(blk[:, 0] == runs) and torch.all(blk[:, 1] == runs)
+    assert torch.all(blk[:, 2] == 1) and torch.all(blk[:, 3] == 0) and torch.all(blk[:, 4] == 0)
 
 
 def test_relay_wait_bound_reports_timeout(gpu):
