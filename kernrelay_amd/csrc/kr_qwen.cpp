@@ -1125,13 +1125,18 @@ std::string Model::ProfileMany(const std::string &spec_path)
             cases.push_back(err.Dump());
             continue;
         }
+        // The graph holds `repeats` back-to-back copies of the k slices and
+        // is replayed once per sample: a graph launch costs more than most
+        // of these kernels on this device, and a prefill replays one graph
+        // for the whole model, so per-launch graph overhead is not op cost.
+        const int repeats = 20;
         hipGraph_t graph = nullptr;
         hipGraphExec_t exec = nullptr;
         Check(hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal), "profile capture");
-        for (auto &f : calls) f(st);
+        for (int r = 0; r < repeats; ++r)
+            for (auto &f : calls) f(st);
         Check(hipStreamEndCapture(st, &graph), "profile capture end");
         Check(hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0), "profile instantiate");
-        const int repeats = 20;
         for (int i = 0; i < 2; ++i) {
             Check(hipGraphLaunch(exec, st), "profile warmup");
             Check(hipStreamSynchronize(st), "profile warmup sync");
@@ -1140,10 +1145,10 @@ std::string Model::ProfileMany(const std::string &spec_path)
         Check(hipEventCreate(&e0), "event");
         Check(hipEventCreate(&e1), "event");
         std::vector<double> dev, wall, host;
-        for (int it = 0; it < 3; ++it) {
+        for (int it = 0; it < 5; ++it) {
             Check(hipEventRecord(e0, st), "record");
             const auto t0 = Clock::now();
-            for (int r = 0; r < repeats; ++r) Check(hipGraphLaunch(exec, st), "profile replay");
+            Check(hipGraphLaunch(exec, st), "profile replay");
             const auto te = Clock::now();
             Check(hipEventRecord(e1, st), "record");
             Check(hipStreamSynchronize(st), "profile sync");
