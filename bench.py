@@ -132,6 +132,7 @@ def main():
     ap.add_argument("--seq", type=int, default=2048)
     ap.add_argument("--preset", default="qwen2.5-7b")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--no-dag", action="store_true", help="skip the mm -> consumer DAG workloads")
     ap.add_argument("--keep", default=None, help="keep / reuse the model directory here")
     ap.add_argument("--profile-gemm", nargs=3, type=int, metavar=("M", "N", "K"),
                     help="only launch the producer GEMM --reps times (for rocprofv3 --pmc)")
@@ -188,6 +189,11 @@ def main():
         total_serial_s = sum(serial["samples_us"]) / 1e6
         value = args.steps * S / total_split_s
         flops = modeldir.model_flops(cfg, S)
+        dag = None
+        if not args.no_dag:
+            from kernrelay_amd import dag_bench
+            log("DAG workloads: tiny mm->GELU, 4096^3 mm -> {softmax, gelu, cast} at k=1,2,4,8")
+            dag = dag_bench.run_all()
         cpu = None
         if not args.no_cpu:
             log("cpu baseline (oracle, bounded sample)")
@@ -210,6 +216,7 @@ def main():
             "prefill_mfma_frac": round(flops / (total_split_s / args.steps) / 1e12 / PEAK_BF16_TFLOPS, 4),
             "roofline": roof,
             "cpu_baseline": cpu,
+            "dag": dag,
             "bit_exact_serial_vs_split": True,
             "argmax": split["argmax"], "flag_edges": split["flag_edges"], "flag_timeouts": split["flag_timeouts"],
         }

@@ -100,6 +100,19 @@ __device__ __forceinline__ uint16_t F32ToBF16(float f)
     return __builtin_bit_cast(uint16_t, static_cast<__bf16>(f));
 }
 
+// Workgroup id -> logical work index, XCD-aware. The dispatcher deals
+// workgroups to the 8 XCDs round-robin (XCD = blockIdx % 8), each with its
+// own L2. Within the run of `per` consecutive ids from `first`, the ids an
+// XCD receives map to one contiguous chunk of [0, per), so neighbouring work
+// items (sharing operands) run under one L2. A bijection on [0, per).
+__device__ __forceinline__ int XcdChunk(int bid, int first, int per)
+{
+    const int off = (bid - first) & 7;
+    const int slot = (bid - first) >> 3;
+    const int q = per >> 3, rem = per & 7;
+    return off < rem ? off * (q + 1) + slot : rem * (q + 1) + (off - rem) * q + slot;
+}
+
 // Fast transcendental building blocks on the hardware's v_exp_f32 (2^x) and
 // v_rcp_f32 (about 1 ulp each): far below the 16-bit rounding that follows
 // every use, and the same instructions in every schedule (split or not).

@@ -67,13 +67,6 @@ __device__ __forceinline__ int Swz(int row, int chunk) { return chunk ^ ((row >>
 //   of the rows is complete first; each run covers order_rows/bm row blocks,
 //   odd runs with the weight columns in reverse (each run reads all of the
 //   weight, and the blocks the last run read are the ones still cached).
-__device__ __forceinline__ int XcdChunk(int bid, int first, int per)
-{
-    const int off = (bid - first) & 7;
-    const int slot = (bid - first) >> 3;
-    const int q = per >> 3, rem = per & 7;
-    return off < rem ? off * (q + 1) + slot : rem * (q + 1) + (off - rem) * q + slot;
-}
 
 __device__ __forceinline__ void TileOf(int bid, int tiles_m, int tiles_n, int bm, int order_rows, int &tm, int &tn)
 {

@@ -1,0 +1,153 @@
+"""The mm -> consumer DAG workloads through kr_plan_run on one GPU.
+
+* tiny mm->GELU: X[256,512] . W[512,512] -> GELU-tanh, producer split k=2
+  (latency-bound; reported for reference, parity is the point);
+* fan-out: X[4096,4096] . W[4096,4096] -> {row softmax, GELU, bf16->fp16
+  cast} per row tile, serial (one stream), B0 (two streams, unsplit) and the
+  relay split at k = 1, 2, 4, 8 (schedules from kernrelay_amd.schedule, as
+  the reference's E3/E4 variants, python/kernrelay/e34.py:16-22).
+
+Each variant runs as a replayed graph per stream (`graph_per_stream`); the
+reported time is the device makespan (HIP events on both streams, best and
+median of the timed runs). Every variant's checksum must equal the serial
+one (the relay changes when rows are computed, never what they hold).
+
+Also reported: the producer GEMM alone (MFMA fraction of the 2.5 PFLOP/s
+bf16 peak) and each consumer alone (GB/s of its algorithmic read + write
+bytes against 8 TB/s).
+
+    python -m kernrelay_amd.dag_bench [--iters 20]
+"""
+
+import argparse
+import contextlib
+import ctypes
+import json
+import os
+import sys
+import tempfile
+from pathlib import Path
+
+from . import libapi, schedule, workloads
+
+PEAK_BF16_TFLOPS = 2500.0
+PEAK_HBM_GBS = 8000.0
+
+
+@contextlib.contextmanager
+def _stdout_to_stderr():
+    """kr_plan_run prints its result line on stdout (as the reference's
+    executor does); keep it off this process's stdout, which carries one
+    JSON line."""
+    libc = ctypes.CDLL(None)
+    sys.stdout.flush()
+    libc.fflush(None)
+    saved = os.dup(1)
+    os.dup2(2, 1)
+    try:
+        yield
+    finally:
+        libc.fflush(None)
+        os.dup2(saved, 1)
+        os.close(saved)
+
+
+def _plan(sched, tmp, name, iters, warmup, mode="graph_per_stream"):
+    path = schedule.dump_schedule(sched, Path(tmp) / (name + ".json"))
+    with _stdout_to_stderr():
+        r = libapi.plan_run(path, devices="0", mode=mode, iters=iters, warmup=warmup,
+                            out_json=Path(tmp) / (name + "_out.json"))
+    if r.get("_rc") != 0 or not r.get("ok"):
+        raise RuntimeError("kr_plan_run %s failed: %s" % (name, r))
+    return r
+
+
+def _times(r):
+    return {"device_best_us": round(r["device_best_us"], 2),
+            "device_p50_us": round(r["device_p50_us"], 2),
+            "wall_p50_us": round(r["p50_us"], 2)}
+
+
+def fanout(tmp, M=4096, K=4096, N=4096, ks=(1, 2, 4, 8), iters=20, warmup=3):
+    dag = workloads.mm_fanout(tmp, M, K, N)
+    serial = _plan(schedule.serial_schedule(dag), tmp, "serial", iters, warmup)
+    out = {"shape": [M, K, N], "consumers": ["softmax", "gelu", "cast"],
+           "serial": _times(serial), "checksum": serial["checksum"]}
+    b0 = _plan(workloads.variants(dag, 1)["b0"], tmp, "b0", iters, warmup)
+    out["b0"] = _times(b0)
+    same = [b0["checksum"] == serial["checksum"]]
+    out["split"] = {}
+    for k in ks:
+        r = _plan(workloads.variants(dag, k)["split"], tmp, "split%d" % k, iters, warmup)
+        same.append(r["checksum"] == serial["checksum"])
+        t = _times(r)
+        t["vs_serial"] = round(serial["device_best_us"] / r["device_best_us"], 4)
+        t["vs_b0"] = round(b0["device_best_us"] / r["device_best_us"], 4)
+        out["split"][str(k)] = t
+    out["checksums_equal"] = all(same)
+    return out
+
+
+def tiny(tmp, iters=50, warmup=5):
+    dag = workloads.tiny_mm_gelu(tmp)
+    serial = _plan(schedule.serial_schedule(dag), tmp, "tiny_serial", iters, warmup)
+    split = _plan(workloads.variants(dag, 2)["split"], tmp, "tiny_split2", iters, warmup)
+    return {"shape": [256, 512, 512], "serial": _times(serial), "split2": _times(split),
+            "checksums_equal": serial["checksum"] == split["checksum"]}
+
+
+def _event_us(fn, reps=10):
+    import torch
+    fn()
+    torch.cuda.synchronize()
+    best = float("inf")
+    for _ in range(3):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        best = min(best, e0.elapsed_time(e1) * 1e3 / reps)
+    return best
+
+
+def kernels_alone(M=4096, K=4096, N=4096):
+    import torch
+    from . import ops
+    g = torch.Generator(device="cuda").manual_seed(1234)
+    A = torch.randn(M, K, device="cuda", generator=g).to(torch.bfloat16)
+    Bt = (torch.randn(N, K, device="cuda", generator=g) * 0.02).to(torch.bfloat16)
+    C = torch.empty(M, N, device="cuda", dtype=torch.bfloat16)
+    us = _event_us(lambda: ops.gemm(A, Bt, C))
+    tf = 2.0 * M * N * K / (us * 1e-6) / 1e12
+    out = {"gemm": {"us": round(us, 2), "tflops": round(tf, 1),
+                    "mfma_frac": round(tf / PEAK_BF16_TFLOPS, 4)}}
+    y16 = torch.empty(M, N, device="cuda", dtype=torch.bfloat16)
+    yh = torch.empty(M, N, device="cuda", dtype=torch.float16)
+    for name, fn, nbytes in (
+            ("softmax", lambda: ops.rowop("softmax", C, y16), 4 * M * N),
+            ("gelu", lambda: ops.elementwise("gelu", C, y16), 4 * M * N),
+            ("cast", lambda: ops.elementwise("cast", C, yh), 4 * M * N)):
+        us = _event_us(fn)
+        gbs = nbytes / (us * 1e-6) / 1e9
+        out[name] = {"us": round(us, 2), "gbs": round(gbs, 1), "hbm_frac": round(gbs / PEAK_HBM_GBS, 4)}
+    return out
+
+
+def run_all(iters=20):
+    with tempfile.TemporaryDirectory(prefix="kr_dag_") as tmp:
+        return {"tiny_mm_gelu": tiny(tmp), "fanout_4096": fanout(tmp, iters=iters),
+                "alone_4096": kernels_alone()}
+
+
+def main(argv=None):
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--iters", type=int, default=20)
+    args = ap.parse_args(argv)
+    print(json.dumps(run_all(args.iters)), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -218,7 +218,8 @@ def test_embedding(gpu):
     assert torch.equal(out.cpu(), table[ids])
 
 
-@pytest.mark.parametrize("S,HQ,HKV,D", [(128, 2, 2, 64), (256, 4, 2, 128), (200, 14, 2, 64), (384, 4, 1, 128)])
+@pytest.mark.parametrize("S,HQ,HKV,D", [(128, 2, 2, 64), (256, 4, 2, 128), (200, 14, 2, 64), (384, 4, 1, 128),
+                                         (1000, 3, 1, 128), (2048, 28, 4, 128)])
 def test_attention(gpu, S, HQ, HKV, D):
     announce("attention S=%d HQ=%d HKV=%d D=%d" % (S, HQ, HKV, D))
     q = rand((S, HQ, D), 1.0, 20)
