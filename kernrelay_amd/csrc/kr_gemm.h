@@ -26,6 +26,9 @@ struct GemmDesc {
     int tail_cols = 0;
     int tail_tiles = 0;          // relay tiles the tail consumes (0 = all); the
                                  // rest are left to a kernel after the GEMM
+    bool coresident = false;     // a consumer kernel spins on the same CUs while
+                                 // this GEMM runs: use a tile whose workgroup
+                                 // leaves register room beside it (not 256x256)
     int order_rows = 0;          // > 0: produce in runs of this many rows (a
                                  // multiple of pub.rows_per_tile), default
                                  // one run per relay tile
@@ -45,7 +48,9 @@ struct GemmTile {
 };
 
 // Tile the launcher would use for this shape ({-1,-1} when no M tile divides
-// the relay tile).
-GemmTile GemmPickTile(int M, int N, int relay_rows);
+// the relay tile). coresident: skip 256x256, whose four waves take every
+// register of the CU (a workgroup of a concurrently spinning consumer would
+// otherwise keep the CU from the GEMM).
+GemmTile GemmPickTile(int M, int N, int relay_rows, bool coresident = false);
 
 }  // namespace kr

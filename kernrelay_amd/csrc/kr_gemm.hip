@@ -461,7 +461,7 @@ int Waves(int tiles, int slots) { return (tiles + slots - 1) / slots; }
 
 }  // namespace
 
-GemmTile GemmPickTile(int M, int N, int relay_rows)
+GemmTile GemmPickTile(int M, int N, int relay_rows, bool coresident)
 {
     // Candidates from most to least data reuse; take the first that keeps the
     // device busy (>= 2 full waves of workgroups) or, failing that, the one
@@ -473,6 +473,7 @@ GemmTile GemmPickTile(int M, int N, int relay_rows)
     double best_eff = -1.0;
     for (const GemmTile &t : cands) {
         if (relay_rows > 0 && relay_rows % t.bm != 0) continue;
+        if (coresident && t.bm * t.bn >= 256 * 256) continue;
         const int tiles = ((M + t.bm - 1) / t.bm) * ((N + t.bn - 1) / t.bn);
         const int slots = cus * (t.bm * t.bn >= 256 * 128 ? 1 : 2);
         if (tiles >= 2 * slots) return t;
@@ -521,7 +522,7 @@ void GemmLaunch(const GemmDesc &d, hipStream_t stream)
     }
     if (p.wait.ctrl != nullptr && p.wait.prod_rows <= 0) throw std::runtime_error("gemm: wait.prod_rows must be > 0");
     const int relay_rows = d.pub.ctrl != nullptr ? d.pub.rows_per_tile : 0;
-    GemmTile t = GemmPickTile(d.M, d.N, relay_rows);
+    GemmTile t = GemmPickTile(d.M, d.N, relay_rows, d.coresident);
     if (const char *e = std::getenv("KR_GEMM_TILE")) {
         // tile sweep override "BMxBN" (measurement aid; bits are unchanged)
         int bm = 0, bn = 0;

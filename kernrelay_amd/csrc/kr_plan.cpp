@@ -24,6 +24,7 @@
 // (exec_main.cpp:1292-1311).
 #include <algorithm>
 #include <cstdio>
+#include <deque>
 #include <fstream>
 #include <map>
 #include <memory>
@@ -294,6 +295,16 @@ struct Launch {
     int flag = -1;
     hipEvent_t pub_event = nullptr;
     std::vector<hipEvent_t> wait_events;
+    // coalescing: rows per released tile, tasks merged, fused consumer nodes
+    // (fan[0] == node) and each one's state base
+    int64_t pub_rows = 0;
+    int merged = 1;
+    bool coresident = false;
+    std::vector<const NodeSpec *> fan;
+    std::vector<int32_t> fan_states;
+    // persistent-consumer tiles (those released before the producer GEMM's
+    // last round of workgroups); -1 = every tile waits in-kernel
+    int early_tiles = -1;
 };
 
 struct RankCtx {
@@ -309,7 +320,8 @@ public:
         sync_ = EnvStr("KR_SYNC", "flag");
         if (sync_ != "flag" && sync_ != "event") throw std::runtime_error("KR_SYNC must be flag or event");
         wait_kind_ = EnvStr("KR_RELAY_WAIT", "fused");
-        relay_grid_ = EnvInt("KR_RELAY_GRID", 64);
+        relay_grid_ = EnvInt("KR_RELAY_GRID", 256);
+        fan_max_ = EnvInt("KR_PLAN_FAN", kMaxFanOut);
         max_spins_ = uint32_t(EnvInt("KR_MAX_SPINS", int(kDefaultMaxSpins)));
         if (mode_ != "direct" && mode_ != "graph" && mode_ != "graph_per_stream")
             throw std::runtime_error("mode '" + mode_ + "' is not built (direct, graph, graph_per_stream)");
@@ -337,6 +349,9 @@ public:
     {
         ValidateGeometry();
         Check(hipSetDevice(device_), "hipSetDevice");
+        Check(hipDeviceGetAttribute(&ncu_, hipDeviceAttributeMultiprocessorCount, device_), "CU count");
+        // a persistent consumer beside a GEMM: at most one workgroup per CU
+        relay_grid_ = std::max(1, std::min(relay_grid_, ncu_));
         streams_.Create(device_);
         Check(hipEventCreate(&ev0_), "event");
         Check(hipEventCreate(&ev1_), "event");
@@ -543,20 +558,180 @@ private:
 
     int NodeTiles(const NodeSpec &n) const { return n.split ? n.tiles : 1; }
 
+    int64_t TaskRows(const TaskSpec &t) const
+    {
+        const NodeSpec &n = doc_.Node(t.node);
+        return t.has_geom ? t.in_rows : n.rows / NodeTiles(n);
+    }
+    int64_t TaskInOff(const TaskSpec &t) const
+    {
+        const NodeSpec &n = doc_.Node(t.node);
+        return t.has_geom ? t.in_row_off : t.tile * (n.rows / NodeTiles(n));
+    }
+    int64_t TaskOutOff(const TaskSpec &t) const
+    {
+        const NodeSpec &n = doc_.Node(t.node);
+        return t.has_geom ? t.out_row_off : t.tile * (n.rows / NodeTiles(n));
+    }
+
+    // A consumer task whose waits can be taken inside its own kernel: all on
+    // one producer node, exactly the producer tiles its input rows intersect.
+    bool InKernelWait(const TaskSpec &t, std::string *prod) const
+    {
+        if (t.waits.empty()) return false;
+        const std::string &p = t.waits[0].first;
+        std::vector<int> tiles;
+        for (const auto &w : t.waits) {
+            if (w.first != p) return false;
+            tiles.push_back(w.second);
+        }
+        std::sort(tiles.begin(), tiles.end());
+        const NodeSpec &P = doc_.Node(p);
+        const int ptiles = NodeTiles(P);
+        const int64_t prows = OutRows(P) / ptiles;
+        const int64_t lo = TaskInOff(t), hi = lo + TaskRows(t);
+        std::vector<int> hits;
+        for (int k = 0; k < ptiles; ++k)
+            if (k * prows < hi && (k + 1) * prows > lo) hits.push_back(k);
+        if (hits != tiles) return false;
+        if (prod) *prod = p;
+        return true;
+    }
+
+    // Task t continues `run` (consecutive tasks of one lane) as one launch:
+    // the next row tile of the same node, contiguous rows, and either a GEMM
+    // with no waits (one launch releasing each tile in turn) or a consumer
+    // waiting in-kernel on one producer (one persistent launch that waits for
+    // each tile in turn).
+    bool Extends(const std::vector<const TaskSpec *> &run, const TaskSpec &t) const
+    {
+        const TaskSpec &a = *run.back();
+        if (t.node != a.node || t.tile != a.tile + 1 || t.publish != a.publish) return false;
+        if (a.n_tile > 0 || t.n_tile > 0) return false;
+        if (TaskRows(t) != TaskRows(a) || TaskInOff(t) != TaskInOff(a) + TaskRows(a) ||
+            TaskOutOff(t) != TaskOutOff(a) + TaskRows(a))
+            return false;
+        const NodeSpec &n = doc_.Node(t.node);
+        if (n.op == Op::MatMul) return a.waits.empty() && t.waits.empty();
+        if (t.publish || wait_kind_ != "fused") return false;
+        std::string pa, pt;
+        return InKernelWait(a, &pa) && InKernelWait(t, &pt) && pa == pt;
+    }
+
+    static bool FanOp(Op op)
+    {
+        return op == Op::Gelu || op == Op::Silu || op == Op::Cast || op == Op::Softmax || op == Op::RmsNorm;
+    }
+
+    // Run r holds the same rows of another unary consumer of the producer
+    // the runs of `group` consume: read the rows once for all of them.
+    bool Sibling(const std::vector<std::vector<const TaskSpec *>> &group, const std::vector<const TaskSpec *> &r) const
+    {
+        if (int(group.size()) >= kMaxFanOut || fan_max_ < 2 || int(group.size()) >= fan_max_) return false;
+        const auto &r0 = group[0];
+        const NodeSpec &a = doc_.Node(r0[0]->node), &b = doc_.Node(r[0]->node);
+        if (!FanOp(a.op) || !FanOp(b.op) || a.preds.size() != 1 || b.preds.size() != 1 || a.preds[0] != b.preds[0])
+            return false;
+        if (a.dtype != b.dtype || a.cols != b.cols || r.size() != r0.size()) return false;
+        for (size_t i = 0; i < r.size(); ++i) {
+            const TaskSpec &x = *r0[i], &y = *r[i];
+            if (x.publish || y.publish || TaskInOff(x) != TaskInOff(y) || TaskRows(x) != TaskRows(y) ||
+                TaskOutOff(x) != TaskOutOff(y))
+                return false;
+            std::string px, py;
+            if (!InKernelWait(x, &px) || !InKernelWait(y, &py) || px != py || px != a.preds[0]) return false;
+            auto wx = x.waits, wy = y.waits;
+            std::sort(wx.begin(), wx.end());
+            std::sort(wy.begin(), wy.end());
+            if (wx != wy) return false;
+        }
+        return true;
+    }
+
+    // How many leading tiles of consumer launch L its producer launch PL
+    // releases before its last round of workgroups starts: a persistent
+    // consumer beside the GEMM can only overlap those; the rest are released
+    // when the GEMM ends and run better at full width. -1 when PL is not one
+    // GEMM launch releasing every tile of its node (then every tile waits
+    // in-kernel).
+    int EarlyTiles(const Launch &PL, const Launch &L, int64_t in_off, int64_t in_rows) const
+    {
+        const NodeSpec &P = *PL.node;
+        if (P.op != Op::MatMul || !PL.publish || PL.merged != NodeTiles(P) || PL.task->n_tile > 0) return -1;
+        const int64_t prows = PL.pub_rows;
+        if (prows <= 0 || L.tile_rows != prows || in_off % prows != 0) return -1;
+        const int M = int(TaskRows(*PL.task)), N = int(P.n);
+        const GemmTile gt = GemmPickTile(M, N, int(prows), true);
+        if (gt.bm <= 0) return -1;
+        const int64_t tn = (N + gt.bn - 1) / gt.bn;
+        const int64_t per = (prows / gt.bm) * tn;                 // workgroups per relay tile
+        const int64_t total = ((M + gt.bm - 1) / gt.bm) * tn;
+        const int64_t slots = int64_t(ncu_) * (gt.bm * gt.bn >= 256 * 128 ? 1 : 2);
+        const int64_t last_round = ((total - 1) / slots) * slots;  // first workgroup of the last round
+        const int k0 = int(in_off / prows);
+        const int nt = int((in_rows + prows - 1) / prows);
+        int early = 0;
+        while (early < nt && (int64_t(k0 + early) + 1) * per <= last_round) ++early;
+        return early;
+    }
+
     void Wire()
     {
-        // launches in per-lane order
+        // Launches. With device flags, consecutive row tiles of one node
+        // become one launch (a GEMM that releases each tile as it completes,
+        // or a persistent consumer that waits for each in turn), and sibling
+        // unary consumers of the same producer rows share one pass over them
+        // (KR_PLAN_COALESCE=0 keeps one launch per task, as the reference).
+        const bool coalesce = sync_ == "flag" && EnvInt("KR_PLAN_COALESCE", 1) != 0;
         std::map<Key, size_t> launch_of;
-        for (size_t l = 0; l < doc_.lanes.size(); ++l)
+        for (size_t l = 0; l < doc_.lanes.size(); ++l) {
+            std::vector<std::vector<const TaskSpec *>> runs;
             for (const auto &t : doc_.lanes[l].tasks) {
+                if (coalesce && !runs.empty() && Extends(runs.back(), t)) {
+                    runs.back().push_back(&t);
+                } else {
+                    runs.push_back({&t});
+                }
+            }
+            std::vector<std::vector<std::vector<const TaskSpec *>>> groups;
+            for (auto &r : runs) {
+                if (coalesce && !groups.empty() && Sibling(groups.back(), r)) {
+                    groups.back().push_back(r);
+                } else {
+                    groups.push_back({r});
+                }
+            }
+            for (const auto &g : groups) {
                 Launch L;
                 L.lane = LaneOf(doc_.lanes[l].engine);
-                L.task = &t;
-                L.node = &doc_.Node(t.node);
-                L.publish = t.publish;
-                launch_of[{t.node, t.tile}] = launches_.size();
+                const auto &r0 = g[0];
+                if (r0.size() == 1) {
+                    L.task = r0[0];
+                } else {
+                    TaskSpec m = *r0[0];
+                    m.has_geom = true;
+                    m.in_row_off = TaskInOff(*r0[0]);
+                    m.out_row_off = TaskOutOff(*r0[0]);
+                    m.in_rows = 0;
+                    m.waits.clear();
+                    for (const TaskSpec *t : r0) {
+                        m.in_rows += TaskRows(*t);
+                        for (const auto &w : t->waits)
+                            if (std::find(m.waits.begin(), m.waits.end(), w) == m.waits.end()) m.waits.push_back(w);
+                    }
+                    merged_.push_back(m);
+                    L.task = &merged_.back();
+                }
+                L.node = &doc_.Node(r0[0]->node);
+                L.publish = L.task->publish;
+                L.pub_rows = TaskRows(*r0[0]);
+                L.merged = int(r0.size());
+                for (const auto &r : g) L.fan.push_back(&doc_.Node(r[0]->node));
+                for (const auto &r : g)
+                    for (const TaskSpec *t : r) launch_of[{t->node, t->tile}] = launches_.size();
                 launches_.push_back(L);
             }
+        }
         if (doc_.lanes.size() > 2) throw std::runtime_error("more than two engine lanes after normalization");
         // Which tasks are awaited: only cross-lane waits need a flag/event.
         std::map<std::string, int> flag_base;
@@ -576,12 +751,14 @@ private:
                 if (it == launch_of.end()) throw std::runtime_error("missing plan for task " + w.first);
                 const Launch &P = launches_[it->second];
                 if (!P.task->publish) throw std::runtime_error("wait on unpublished flag " + w.first + "#" + std::to_string(w.second));
-                const auto sk = std::make_pair(L.node->id, w.first);
-                if (!state_base.count(sk)) {
-                    state_base[sk] = next_block;
-                    next_block += NodeTiles(doc_.Node(w.first));
+                for (const NodeSpec *c : L.fan) {
+                    const auto sk = std::make_pair(c->id, w.first);
+                    if (!state_base.count(sk)) {
+                        state_base[sk] = next_block;
+                        next_block += NodeTiles(doc_.Node(w.first));
+                    }
+                    last_waiter[std::make_tuple(c->id, w.first, w.second)] = i;
                 }
-                last_waiter[std::make_tuple(L.node->id, w.first, w.second)] = i;
             }
         }
         ctrl_words_ = size_t(std::max(next_block, 1)) * kWords;
@@ -593,10 +770,13 @@ private:
             Launch &L = launches_[i];
             const NodeSpec &n = *L.node;
             const TaskSpec &t = *L.task;
-            const int64_t rt = n.rows / NodeTiles(n);
-            const int64_t in_off = t.has_geom ? t.in_row_off : t.tile * rt;
-            const int64_t in_rows = t.has_geom ? t.in_rows : rt;
-            if (L.publish) L.flag = flag_base.at(n.id) + t.tile;
+            const int64_t in_off = TaskInOff(t);
+            const int64_t in_rows = TaskRows(t);
+            if (L.publish) {
+                L.flag = flag_base.at(n.id) + t.tile;
+                // a GEMM released tile by tile while a consumer spins beside it
+                L.coresident = n.op == Op::MatMul;
+            }
             if (sync_ == "event") {
                 if (L.publish) Check(hipEventCreateWithFlags(&L.pub_event, hipEventDisableTiming), "event");
                 continue;
@@ -609,13 +789,18 @@ private:
                 std::sort(kv.second.begin(), kv.second.end());
                 const int ptiles = NodeTiles(P);
                 const int64_t prows = OutRows(P) / ptiles;
-                const int sbase = state_base.at({n.id, P.id});
+                // per fused consumer: its state base and the tiles it consumes here
+                std::vector<int> sbases;
                 std::vector<int> adv;
-                for (int k : kv.second)
-                    if (last_waiter.at(std::make_tuple(n.id, P.id, k)) == i) {
-                        adv.push_back(k);
-                        consumed_states_.push_back(sbase + k);
-                    }
+                for (size_t c = 0; c < L.fan.size(); ++c) {
+                    const int sb = state_base.at({L.fan[c]->id, P.id});
+                    sbases.push_back(sb);
+                    for (int k : kv.second)
+                        if (last_waiter.at(std::make_tuple(L.fan[c]->id, P.id, k)) == i) {
+                            if (c == 0) adv.push_back(k);
+                            consumed_states_.push_back(sb + k);
+                        }
+                }
                 // tiles intersecting this task's input rows in P's output row space
                 std::vector<int> hits;
                 for (int k = 0; k < ptiles; ++k)
@@ -628,27 +813,32 @@ private:
                     L.fused_wait = true;
                     L.wait.ctrl = ctrl;
                     L.wait.flag0 = flag_base.at(P.id);
-                    L.wait.state0 = sbase;
+                    L.wait.state0 = sbases[0];
                     L.wait.prod_rows = int(prows);
                     L.wait.row_off = int(in_off);
                     L.wait.adv_lo = adv.empty() ? 0 : adv.front();
                     L.wait.adv_hi = adv.empty() ? 0 : adv.back() + 1;
                     L.wait.max_spins = max_spins_;
                     L.tile_rows = int(std::min<int64_t>(in_rows, prows));
+                    L.fan_states = sbases;
+                    L.early_tiles = EarlyTiles(launches_[launch_of.at({P.id, kv.second.front()})], L, in_off, in_rows);
                 } else {
-                    for (int k : kv.second) {
-                        RelayWait w{};
-                        w.ctrl = ctrl;
-                        w.flag0 = flag_base.at(P.id) + k;
-                        w.state0 = sbase + k;
-                        w.prod_rows = 1;
-                        w.row_off = 0;
-                        const bool advance = std::find(adv.begin(), adv.end(), k) != adv.end();
-                        w.adv_lo = 0;
-                        w.adv_hi = advance ? 1 : 0;
-                        w.max_spins = max_spins_;
-                        L.extra_waits.push_back(w);
-                    }
+                    // one-workgroup wait kernels before the launch, one per
+                    // (consumer, producer tile)
+                    for (size_t c = 0; c < L.fan.size(); ++c)
+                        for (int k : kv.second) {
+                            RelayWait w{};
+                            w.ctrl = ctrl;
+                            w.flag0 = flag_base.at(P.id) + k;
+                            w.state0 = sbases[c] + k;
+                            w.prod_rows = 1;
+                            w.row_off = 0;
+                            const bool advance = last_waiter.at(std::make_tuple(L.fan[c]->id, P.id, k)) == i;
+                            w.adv_lo = 0;
+                            w.adv_hi = advance ? 1 : 0;
+                            w.max_spins = max_spins_;
+                            L.extra_waits.push_back(w);
+                        }
                 }
             }
         }
@@ -656,73 +846,69 @@ private:
             for (auto &L : launches_)
                 for (const auto &w : L.task->waits) L.wait_events.push_back(launches_[launch_of.at(w)].pub_event);
         }
-        // enqueue order: global topological order (records before waits)
+        // enqueue order: global topological order (records before waits); a
+        // merged launch goes where its first task would
         auto order = TopoOrder(doc_);
+        std::set<size_t> queued;
         for (const auto &o : order) {
             const auto &t = doc_.lanes[o.first].tasks[o.second];
-            enqueue_order_.push_back(launch_of.at({t.node, t.tile}));
+            const size_t li = launch_of.at({t.node, t.tile});
+            if (queued.insert(li).second) enqueue_order_.push_back(li);
         }
     }
 
     hipStream_t StreamOf(int lane) const { return lane == 0 ? streams_.prod : streams_.cons; }
 
-    void EnqueueTask(RankCtx &rc, Launch &L, hipStream_t s)
+    // One consumer kernel over rows [r0, r0 + nrows) of launch L (local
+    // numbering), waiting in-kernel through `wait` (ctrl == nullptr: none).
+    void LaunchConsumer(RankCtx &rc, Launch &L, hipStream_t s, int64_t r0, int64_t nrows, const RelayWait &wait,
+                        int grid, const RelayPub &pub)
     {
         const NodeSpec &n = *L.node;
         const TaskSpec &t = *L.task;
         NodeBuf &b = rc.bufs.at(n.id);
-        const int64_t rt = n.rows / NodeTiles(n);
-        const int64_t in_off = t.has_geom ? t.in_row_off : t.tile * rt;
-        const int64_t in_rows = t.has_geom ? t.in_rows : rt;
-        const int64_t out_off = t.has_geom ? t.out_row_off : t.tile * rt;
+        const int64_t in_off = TaskInOff(t) + r0;
+        const int64_t out_off = TaskOutOff(t) + r0;
         const void *in_base = n.preds.empty() ? b.own_in.get() : rc.bufs.at(n.preds[0]).out.get();
-        const size_t in_elem = 2;
-        const auto *in_tile = static_cast<const char *>(in_base) + size_t(in_off) * InCols(n) * in_elem;
+        const auto *in_tile = static_cast<const char *>(in_base) + size_t(in_off) * InCols(n) * 2;
         const void *x1 = nullptr;
         if (IsBinary(n.op)) {
             const void *x1base = n.preds.size() > 1 ? rc.bufs.at(n.preds[1]).out.get() : b.aux.get();
             x1 = static_cast<const char *>(x1base) + size_t(in_off) * n.cols * 2;
         }
         char *out_tile = static_cast<char *>(b.out.get()) + size_t(out_off) * n.cols * DTypeBytes(n.out_dtype);
+        const int tile_rows = wait.ctrl != nullptr ? L.tile_rows : 0;
 
-        if (sync_ == "event") {
-            for (hipEvent_t e : L.wait_events) Check(hipStreamWaitEvent(s, e, 0), "stream wait event");
-        }
-        for (const auto &w : L.extra_waits) WaitLaunch(w, 0, 1, s);
-
-        RelayPub pub{};
-        if (L.publish && sync_ == "flag") {
-            pub.ctrl = ctrl_.as<int32_t>();
-            pub.flag0 = L.flag;
-            pub.rows_per_tile = int(in_rows);
-        }
-        const RelayWait wait = L.fused_wait ? L.wait : RelayWait{};
-        const int grid = L.fused_wait ? relay_grid_ : 0;
-
-        switch (n.op) {
-            case Op::MatMul: {
-                GemmDesc d;
-                d.dtype = n.dtype;
-                d.A = in_tile;
-                d.lda = n.k;
-                const int64_t ncols = t.n_tile > 0 ? t.n_tile : n.n;
-                d.Bt = b.bt.as<uint16_t>() + size_t(t.n_off) * n.k;
-                d.ldb = n.k;
-                d.C = reinterpret_cast<uint16_t *>(out_tile) + (t.n_tile > 0 ? t.n_off : 0);
-                d.ldc = n.n;
-                d.M = int(in_rows);
-                d.N = int(ncols);
-                d.K = int(n.k);
-                if (pub.ctrl && GemmPickTile(d.M, d.N, pub.rows_per_tile).bm < 0) {
-                    // the tile cannot be one GEMM relay tile: release after the GEMM
-                    GemmLaunch(d, s);
-                    PublishLaunch(pub, 0, s);
-                } else {
-                    d.pub = pub;
-                    GemmLaunch(d, s);
-                }
-                break;
+        if (L.fan.size() > 1) {
+            // sibling unary consumers of the same rows: one pass, every output
+            FanDesc d;
+            d.dtype_in = n.dtype;
+            d.x = in_tile;
+            d.rows = int(nrows);
+            d.cols = int(n.cols);
+            d.eps = n.eps;
+            d.n_out = int(L.fan.size());
+            for (size_t i = 0; i < L.fan.size(); ++i) {
+                const NodeSpec &c = *L.fan[i];
+                NodeBuf &cb = rc.bufs.at(c.id);
+                FanOutDesc &o = d.out[i];
+                o.op = c.op == Op::Gelu ? kEwGelu
+                     : c.op == Op::Silu ? kEwSilu
+                     : c.op == Op::Cast ? kEwCast
+                     : c.op == Op::Softmax ? kFanSoftmax
+                                           : kFanRmsNorm;
+                o.dtype = c.out_dtype;
+                o.y = static_cast<char *>(cb.out.get()) + size_t(out_off) * c.cols * DTypeBytes(c.out_dtype);
+                o.gamma = cb.gamma.get();
+                d.states[i] = L.fan_states.empty() ? 0 : L.fan_states[i];
             }
+            d.tile_rows = tile_rows;
+            d.grid = grid;
+            d.wait = wait;
+            FanLaunch(d, s);
+            return;
+        }
+        switch (n.op) {
             case Op::Gelu:
             case Op::Silu:
             case Op::Cast:
@@ -741,9 +927,9 @@ private:
                 d.x0 = in_tile;
                 d.x1 = x1;
                 d.y = out_tile;
-                d.rows = int(in_rows);
+                d.rows = int(nrows);
                 d.cols = int(n.cols);
-                d.tile_rows = L.fused_wait ? L.tile_rows : 0;
+                d.tile_rows = tile_rows;
                 d.grid = grid;
                 d.wait = wait;
                 d.pub = pub;
@@ -768,10 +954,10 @@ private:
                 d.gamma = b.gamma.get();
                 d.y = out_tile;
                 d.sum_out = b.sum.get() ? static_cast<char *>(b.sum.get()) + size_t(out_off) * n.cols * 2 : nullptr;
-                d.rows = int(in_rows);
+                d.rows = int(nrows);
                 d.cols = int(n.cols);
                 d.eps = n.eps;
-                d.tile_rows = L.fused_wait ? L.tile_rows : 0;
+                d.tile_rows = tile_rows;
                 d.grid = grid;
                 d.wait = wait;
                 d.pub = pub;
@@ -783,6 +969,79 @@ private:
                     RowLaunch(d, s);
                 }
                 break;
+            }
+            case Op::MatMul:
+                throw std::logic_error("LaunchConsumer: matmul");
+        }
+    }
+
+    void EnqueueTask(RankCtx &rc, Launch &L, hipStream_t s)
+    {
+        const NodeSpec &n = *L.node;
+        const TaskSpec &t = *L.task;
+        NodeBuf &b = rc.bufs.at(n.id);
+        const int64_t in_off = TaskInOff(t);
+        const int64_t in_rows = TaskRows(t);
+        const int64_t out_off = TaskOutOff(t);
+
+        if (sync_ == "event") {
+            for (hipEvent_t e : L.wait_events) Check(hipStreamWaitEvent(s, e, 0), "stream wait event");
+        }
+        for (const auto &w : L.extra_waits) WaitLaunch(w, 0, 1, s);
+
+        RelayPub pub{};
+        if (L.publish && sync_ == "flag") {
+            pub.ctrl = ctrl_.as<int32_t>();
+            pub.flag0 = L.flag;
+            pub.rows_per_tile = int(L.pub_rows > 0 ? L.pub_rows : in_rows);
+        }
+
+        if (n.op == Op::MatMul) {
+            const void *in_base = n.preds.empty() ? b.own_in.get() : rc.bufs.at(n.preds[0]).out.get();
+            GemmDesc d;
+            d.dtype = n.dtype;
+            d.A = static_cast<const char *>(in_base) + size_t(in_off) * n.k * 2;
+            d.lda = n.k;
+            const int64_t ncols = t.n_tile > 0 ? t.n_tile : n.n;
+            d.Bt = b.bt.as<uint16_t>() + size_t(t.n_off) * n.k;
+            d.ldb = n.k;
+            d.C = reinterpret_cast<uint16_t *>(static_cast<char *>(b.out.get()) + size_t(out_off) * n.cols * 2) +
+                  (t.n_tile > 0 ? t.n_off : 0);
+            d.ldc = n.n;
+            d.M = int(in_rows);
+            d.N = int(ncols);
+            d.K = int(n.k);
+            d.coresident = L.coresident;
+            if (pub.ctrl && GemmPickTile(d.M, d.N, pub.rows_per_tile, d.coresident).bm < 0) {
+                // the tile cannot be one GEMM relay tile: release after the GEMM
+                GemmLaunch(d, s);
+                for (int k = 0; k < L.merged; ++k) PublishLaunch(pub, k, s);
+            } else {
+                d.pub = pub;
+                GemmLaunch(d, s);
+            }
+        } else if (!L.fused_wait) {
+            LaunchConsumer(rc, L, s, 0, in_rows, RelayWait{}, 0, pub);
+        } else if (L.early_tiles < 0) {
+            // persistent consumer: waits for each producer tile in turn
+            LaunchConsumer(rc, L, s, 0, in_rows, L.wait, relay_grid_, pub);
+        } else {
+            // tiles released before the producer's last round: a persistent
+            // consumer beside the GEMM; tiles released at its end: a wait
+            // kernel, then the consumer at full width
+            const int64_t rows_a = std::min<int64_t>(in_rows, int64_t(L.early_tiles) * L.tile_rows);
+            const int split_tile = int((in_off + rows_a) / L.wait.prod_rows);
+            RelayWait wa = L.wait, wb = L.wait;
+            wa.adv_hi = std::min(wa.adv_hi, split_tile);
+            wb.adv_lo = std::max(wb.adv_lo, split_tile);
+            if (wa.adv_hi < wa.adv_lo) wa.adv_hi = wa.adv_lo;
+            if (wb.adv_hi < wb.adv_lo) wb.adv_hi = wb.adv_lo;
+            if (rows_a > 0) LaunchConsumer(rc, L, s, 0, rows_a, wa, relay_grid_, RelayPub{});
+            if (rows_a < in_rows) {
+                const std::vector<int32_t> st = L.fan_states.empty() ? std::vector<int32_t>{wb.state0} : L.fan_states;
+                wb.state0 = st[0];
+                WaitLaunchMulti(wb, int(rows_a), int(in_rows), st.data(), int(st.size()), s);
+                LaunchConsumer(rc, L, s, rows_a, in_rows - rows_a, RelayWait{}, 0, RelayPub{});
             }
         }
         Check(hipGetLastError(), "task launch");
@@ -853,7 +1112,10 @@ private:
     std::string mode_;
     std::string sync_;
     std::string wait_kind_;
-    int relay_grid_ = 64;
+    int relay_grid_ = 256;
+    int ncu_ = 256;
+    int fan_max_ = kMaxFanOut;
+    std::deque<TaskSpec> merged_;
     uint32_t max_spins_ = kDefaultMaxSpins;
     StreamPair streams_;
     hipEvent_t ev0_ = nullptr, ev1_ = nullptr, ev2_ = nullptr;

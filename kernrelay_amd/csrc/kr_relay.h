@@ -144,6 +144,35 @@ __device__ __forceinline__ void RelayFinish(const RelayWait &w)
     }
 }
 
+// RelayFinish for a launch that stands in for several consumers of the same
+// producer tiles (sibling consumers fused into one kernel): the state blocks
+// of every consumer (bases states[0..n)) advance together over adv_lo..adv_hi.
+// w.state0 must equal states[0] (its `done` word is the completion ticket).
+__device__ __forceinline__ void RelayFinishMulti(const RelayWait &w, const int32_t *states, int n)
+{
+    if (w.ctrl == nullptr || w.adv_hi <= w.adv_lo) return;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        int32_t *ticket = w.ctrl + size_t(w.state0 + w.adv_lo) * kWords + kOffDone;
+        const int32_t t = __hip_atomic_fetch_add(ticket, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (t == int32_t(gridDim.x * gridDim.y * gridDim.z) - 1) {
+            StoreRelaxed(ticket, 0);
+            // a timeout seen by any workgroup is recorded on the first
+            // consumer's state (the one the spins read); every fused consumer
+            // reports it
+            for (int k = w.adv_lo; k < w.adv_hi; ++k) {
+                const int32_t to = __hip_atomic_exchange(w.ctrl + size_t(w.state0 + k) * kWords + kOffTimedOut, 0,
+                                                         __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                for (int i = 0; i < n; ++i) {
+                    int32_t *st = w.ctrl + size_t(states[i] + k) * kWords;
+                    StoreRelaxed(st + kOffConsumed, LoadRelaxed(st + kOffConsumed) + 1);
+                    StoreRelaxed(st + kOffStatus, to ? 2 : 1);
+                }
+            }
+        }
+    }
+}
+
 // Stores of data a relay releases. A producer that publishes writes its
 // outputs with device-scope stores (sc1: written through this XCD's L2 to
 // memory, where every XCD reads it), so a release needs no cache-wide

@@ -65,10 +65,42 @@ struct RowDesc {
 void EwLaunch(const EwDesc &d, hipStream_t stream);
 void RowLaunch(const RowDesc &d, hipStream_t stream);
 
+// Several unary consumers of the same rows fused into one pass: every row of
+// x is read once and each output written from registers. Each output's bits
+// equal its standalone kernel's (same per-element arithmetic; softmax and
+// rmsnorm use RowLaunch's lane layout and reduction tree for these cols).
+// Ops: kEwGelu, kEwSilu, kEwCast (to `dtype`), kFanSoftmax, kFanRmsNorm
+// (gamma). The relay wait is shared; `states` lists every consumer's state
+// base (states[0] == wait.state0), all advanced by this launch.
+enum FanOp : int { kFanSoftmax = 16, kFanRmsNorm = 17 };
+constexpr int kMaxFanOut = 4;
+struct FanOutDesc {
+    int op = kEwGelu;
+    int dtype = kBF16;
+    void *y = nullptr;
+    const void *gamma = nullptr;
+};
+struct FanDesc {
+    int dtype_in = kBF16;
+    const void *x = nullptr;
+    int rows = 0, cols = 0;
+    float eps = 1e-6f;
+    int n_out = 0;
+    FanOutDesc out[kMaxFanOut];
+    int tile_rows = 0;
+    int grid = 0;
+    RelayWait wait{};
+    int32_t states[kMaxFanOut] = {0, 0, 0, 0};
+};
+void FanLaunch(const FanDesc &d, hipStream_t stream);
+
 // Standalone relay kernels (the reference's separate kr_wait_* / kr_publish_*
 // launches): wait for producer rows [lo, hi) and consume edges adv_lo..adv_hi;
 // publish tile `tile` once (arrivals forced to 1).
 void WaitLaunch(const RelayWait &w, int lo, int hi, hipStream_t stream);
+// The same for a launch standing in for n fused consumers (states[0] ==
+// w.state0): every consumer's state blocks adv_lo..adv_hi advance.
+void WaitLaunchMulti(const RelayWait &w, int lo, int hi, const int32_t *states, int n, hipStream_t stream);
 
 
 void PublishLaunch(const RelayPub &p, int tile, hipStream_t stream);

@@ -39,15 +39,16 @@ struct EwParams {
     RelayPub pub;
 };
 
-// tanh(y) = 1 - 2 / (1 + e^(2y)): saturates to +-1 through inf / 0 of the
-// exponential, and its absolute error near 0 (~1e-7) vanishes in 1 + tanh.
+// GELU, tanh form: 0.5 x (1 + tanh(y)), y = sqrt(2/pi) (x + 0.044715 x^3),
+// computed as the identical x / (1 + e^(-2y)) (1 + tanh(y) = 2 / (1 + e^(-2y))):
+// five full-rate operations and two transcendentals per element. Saturates
+// through the exponential: e^(-2y) -> inf gives -0 for large negative x,
+// -> 0 gives x for large positive x.
 __device__ __forceinline__ float GeluTanh(float x)
 {
-    const float k0 = 0.7978845608028654f;  // sqrt(2/pi)
-    const float k1 = 0.044715f;
-    const float y = k0 * (x + k1 * x * x * x);
-    const float t = 1.0f - 2.0f * FastRcp(1.0f + FastExp(2.0f * y));
-    return 0.5f * x * (1.0f + t);
+    const float c = -2.0f * 0.7978845608028654f * 1.4426950408889634f;  // -2 sqrt(2/pi) log2(e)
+    const float u = 1.0f + 0.044715f * (x * x);
+    return x * FastRcp(1.0f + __builtin_amdgcn_exp2f(c * x * u));
 }
 
 
@@ -211,12 +212,14 @@ __global__ void __launch_bounds__(kThreads) RowKernel(RowParams p)
                             s += v[c][e];
                         }
                 s = GroupReduce<LPR, false>(s, red);
+                // one IEEE division per row; every element scales by it
+                const float inv = 1.0f / s;
 #pragma unroll
                 for (int c = 0; c < CPL; ++c) {
                     if (!ok[c]) continue;
                     U16x8 o;
 #pragma unroll
-                    for (int e = 0; e < 8; ++e) o.v[e] = Elem<DT>::Store(v[c][e] / s);
+                    for (int e = 0; e < 8; ++e) o.v[e] = Elem<DT>::Store(v[c][e] * inv);
                     PutU128(p.y + base + (ln + c * LPR) * 8, *reinterpret_cast<const uint4 *>(o.v), coh);
                 }
             } else {
@@ -246,10 +249,177 @@ __global__ void __launch_bounds__(kThreads) RowKernel(RowParams p)
     RelayFinish(p.w);
 }
 
+// ------------------------------------------------- fused sibling consumers
+struct FanOutParams {
+    int op, dtype;
+    void *y;
+    const uint16_t *gamma;
+};
+struct FanParams {
+    const uint16_t *x;
+    int rows, cols, tile_rows, n_tiles;
+    float eps;
+    int n_out;
+    FanOutParams out[kMaxFanOut];
+    RelayWait w;
+    int32_t states[kMaxFanOut];
+};
+
+typedef uint32_t FanU32x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ void FanPut16(uint16_t *p, const U16x8 &r)
+{
+    __builtin_nontemporal_store(*reinterpret_cast<const FanU32x4 *>(r.v), reinterpret_cast<FanU32x4 *>(p));
+}
+
+// Store eight fp32 values of one 16-byte input chunk as output type DTO.
+__device__ __forceinline__ void FanStore(void *y, int64_t elem, int dto, const float (&o)[8])
+{
+    if (dto == kF32) {
+        FanU32x4 *yp = reinterpret_cast<FanU32x4 *>(static_cast<float *>(y) + elem);
+        const FanU32x4 lo = {__float_as_uint(o[0]), __float_as_uint(o[1]), __float_as_uint(o[2]), __float_as_uint(o[3])};
+        const FanU32x4 hi = {__float_as_uint(o[4]), __float_as_uint(o[5]), __float_as_uint(o[6]), __float_as_uint(o[7])};
+        __builtin_nontemporal_store(lo, yp);
+        __builtin_nontemporal_store(hi, yp + 1);
+        return;
+    }
+    U16x8 r;
+    if (dto == kBF16) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) r.v[e] = Elem<kBF16>::Store(o[e]);
+    } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) r.v[e] = Elem<kF16>::Store(o[e]);
+    }
+    FanPut16(static_cast<uint16_t *>(y) + elem, r);
+}
+
+// The row loop, lane layout (LPR lanes per row, CPL chunks per lane) and
+// reduction tree of RowKernel, with every output computed from the one load.
+// At most 128 registers per wave: the kernel spins on the CUs of the GEMM
+// that produces its rows (136 registers per wave for the co-resident tiles),
+// and a CU must hold one workgroup of each; at full width four waves per SIMD
+// keep a 1024-workgroup grid resident in one round.
+// Rows are read once and outputs written once: non-temporal accesses, so the
+// consumer does not evict the operand lines the GEMM beside it reuses.
+template <int DT, int LPR, int CPL>
+__global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) FanKernel(FanParams p)
+{
+    constexpr int RPB = kThreads / LPR;
+    __shared__ float red[4];
+    const int slot = threadIdx.x / LPR;
+    const int ln = threadIdx.x % LPR;
+    const int chunks = p.cols / 8;
+
+    for (int t = 0; t < p.n_tiles; ++t) {
+        const int r_lo = t * p.tile_rows;
+        const int r_hi = min(r_lo + p.tile_rows, p.rows);
+        RelayWaitRows(p.w, r_lo, r_hi);
+        for (int rb = r_lo + int(blockIdx.x) * RPB; rb < r_hi; rb += int(gridDim.x) * RPB) {
+            const int r = rb + slot;
+            const bool active = r < r_hi;
+            const int64_t base = int64_t(active ? r : r_lo) * p.cols;
+            float v[CPL][8];
+            bool ok[CPL];
+#pragma unroll
+            for (int c = 0; c < CPL; ++c) {
+                const int ch = ln + c * LPR;
+                ok[c] = active && ch < chunks;
+                if (ok[c]) {
+                    U16x8 a;
+                    *reinterpret_cast<FanU32x4 *>(a.v) =
+                        __builtin_nontemporal_load(reinterpret_cast<const FanU32x4 *>(p.x + base + ch * 8));
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) v[c][e] = Elem<DT>::Load(a.v[e]);
+                } else {
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) v[c][e] = 0.0f;
+                }
+            }
+            for (int i = 0; i < p.n_out; ++i) {
+                const FanOutParams &o = p.out[i];
+                if (o.op == kFanSoftmax) {
+                    // the last output (FanLaunch orders it so): exponentials
+                    // replace the row in registers, as in RowKernel
+                    float m = -INFINITY;
+#pragma unroll
+                    for (int c = 0; c < CPL; ++c)
+                        if (ok[c])
+#pragma unroll
+                            for (int e = 0; e < 8; ++e) m = fmaxf(m, v[c][e]);
+                    m = GroupReduce<LPR, true>(m, red);
+                    float s = 0.0f;
+#pragma unroll
+                    for (int c = 0; c < CPL; ++c)
+                        if (ok[c])
+#pragma unroll
+                            for (int e = 0; e < 8; ++e) {
+                                v[c][e] = FastExp(v[c][e] - m);
+                                s += v[c][e];
+                            }
+                    s = GroupReduce<LPR, false>(s, red);
+                    const float inv = 1.0f / s;
+#pragma unroll
+                    for (int c = 0; c < CPL; ++c) {
+                        if (!ok[c]) continue;
+                        U16x8 q;
+#pragma unroll
+                        for (int e = 0; e < 8; ++e) q.v[e] = Elem<DT>::Store(v[c][e] * inv);
+                        FanPut16(static_cast<uint16_t *>(o.y) + base + (ln + c * LPR) * 8, q);
+                    }
+                } else if (o.op == kFanRmsNorm) {
+                    float ss = 0.0f;
+#pragma unroll
+                    for (int c = 0; c < CPL; ++c)
+#pragma unroll
+                        for (int e = 0; e < 8; ++e) ss += v[c][e] * v[c][e];
+                    ss = GroupReduce<LPR, false>(ss, red);
+                    const float rstd = 1.0f / sqrtf(ss / float(p.cols) + p.eps);
+#pragma unroll
+                    for (int c = 0; c < CPL; ++c) {
+                        if (!ok[c]) continue;
+                        const int ch = ln + c * LPR;
+                        const U16x8 g = LoadU16x8(o.gamma + ch * 8);
+                        U16x8 q;
+#pragma unroll
+                        for (int e = 0; e < 8; ++e)
+                            q.v[e] = Elem<DT>::Store(Elem<DT>::Load(g.v[e]) * RoundTo<DT>(v[c][e] * rstd));
+                        FanPut16(static_cast<uint16_t *>(o.y) + base + ch * 8, q);
+                    }
+                } else {
+#pragma unroll
+                    for (int c = 0; c < CPL; ++c) {
+                        if (!ok[c]) continue;
+                        float q[8];
+#pragma unroll
+                        for (int e = 0; e < 8; ++e)
+                            q[e] = o.op == kEwGelu ? GeluTanh(v[c][e]) : (o.op == kEwSilu ? Silu(v[c][e]) : v[c][e]);
+                        FanStore(o.y, base + (ln + c * LPR) * 8, o.dtype, q);
+                    }
+                }
+            }
+        }
+    }
+    RelayFinishMulti(p.w, p.states, p.n_out);
+}
+
 __global__ void __launch_bounds__(64) WaitKernel(RelayWait w, int lo, int hi)
 {
     RelayWaitRows(w, lo, hi);
     RelayFinish(w);
+}
+
+struct WaitStates {
+    int32_t s[kMaxFanOut];
+    int n;
+};
+
+// Wait for rows [lo, hi), then consume the edges of every listed consumer
+// (fused sibling consumers share one wait).
+__global__ void __launch_bounds__(64) WaitMultiKernel(RelayWait w, int lo, int hi, WaitStates st)
+{
+    RelayWaitRows(w, lo, hi);
+    RelayFinishMulti(w, st.s, st.n);
 }
 
 __global__ void __launch_bounds__(64) PublishKernel(RelayPub p, int tile) { RelayArrive(p, tile); }
@@ -278,7 +448,14 @@ void RowDispatchT(const RowParams &p, int lpr, int cpl, int grid, hipStream_t s)
 {
     auto go = [&](auto kern) { hipLaunchKernelGGL(kern, dim3(grid), dim3(kThreads), 0, s, p); };
     if (lpr == 16) return go(RowKernel<OP, DT, 16, 1>);
-    if (lpr == 64) return go(RowKernel<OP, DT, 64, 1>);
+    if (lpr == 64) {
+        switch (cpl) {
+            case 1: return go(RowKernel<OP, DT, 64, 1>);
+            case 2: return go(RowKernel<OP, DT, 64, 2>);
+            case 4: return go(RowKernel<OP, DT, 64, 4>);
+            default: return go(RowKernel<OP, DT, 64, 8>);
+        }
+    }
     switch (cpl) {
         case 1: return go(RowKernel<OP, DT, 256, 1>);
         case 2: return go(RowKernel<OP, DT, 256, 2>);
@@ -299,6 +476,13 @@ void CheckAligned(const void *p, const char *what)
 {
     if (reinterpret_cast<uintptr_t>(p) & 15) throw std::runtime_error(std::string(what) + " must be 16-byte aligned");
 }
+
+// Lanes per row for a row of `chunks` 16-byte chunks: up to 4096 16-bit
+// columns one wave owns a row (up to 8 chunks per lane, all in flight at
+// once; reductions stay inside the wave), wider rows take the whole
+// workgroup. The layout fixes the reduction tree, so every kernel that
+// reduces rows of a given width uses this one choice.
+int RowLanes(int chunks) { return chunks <= 16 ? 16 : (chunks <= 512 ? 64 : 256); }
 
 }  // namespace
 
@@ -367,7 +551,7 @@ void RowLaunch(const RowDesc &d, hipStream_t stream)
     p.w = d.wait;
     p.pub = d.pub;
     const int chunks = d.cols / 8;
-    const int lpr = chunks <= 16 ? 16 : (chunks <= 64 ? 64 : 256);
+    const int lpr = RowLanes(chunks);
     int cpl = (chunks + lpr - 1) / lpr;
     cpl = cpl <= 1 ? 1 : (cpl <= 2 ? 2 : (cpl <= 4 ? 4 : 8));
     const int rpb = kThreads / lpr;
@@ -380,6 +564,96 @@ void RowLaunch(const RowDesc &d, hipStream_t stream)
         case kRowAddRmsNorm: return RowDispatch<kRowAddRmsNorm>(d, p, lpr, cpl, grid, stream);
         default: throw std::runtime_error("row op: unknown op");
     }
+}
+
+namespace {
+
+template <int DT>
+void FanDispatch(const FanParams &p, int lpr, int cpl, int grid, hipStream_t s)
+{
+    auto go = [&](auto kern) { hipLaunchKernelGGL(kern, dim3(grid), dim3(kThreads), 0, s, p); };
+    if (lpr == 16) return go(FanKernel<DT, 16, 1>);
+    if (lpr == 64) {
+        switch (cpl) {
+            case 1: return go(FanKernel<DT, 64, 1>);
+            case 2: return go(FanKernel<DT, 64, 2>);
+            case 4: return go(FanKernel<DT, 64, 4>);
+            default: return go(FanKernel<DT, 64, 8>);
+        }
+    }
+    switch (cpl) {
+        case 1: return go(FanKernel<DT, 256, 1>);
+        case 2: return go(FanKernel<DT, 256, 2>);
+        case 4: return go(FanKernel<DT, 256, 4>);
+        default: return go(FanKernel<DT, 256, 8>);
+    }
+}
+
+}  // namespace
+
+void FanLaunch(const FanDesc &d, hipStream_t stream)
+{
+    if (d.rows <= 0 || d.cols <= 0) return;
+    if (d.n_out < 1 || d.n_out > kMaxFanOut) throw std::runtime_error("fan-out: 1..4 outputs");
+    if (d.cols % 8 != 0) throw std::runtime_error("fan-out: cols must be a multiple of 8");
+    if (d.cols > 16384) throw std::runtime_error("fan-out: cols must be <= 16384");
+    if (d.dtype_in != kBF16 && d.dtype_in != kF16) throw std::runtime_error("fan-out: input must be bf16 or f16");
+    CheckAligned(d.x, "fan-out x");
+    FanParams p{};
+    p.x = static_cast<const uint16_t *>(d.x);
+    p.rows = d.rows;
+    p.cols = d.cols;
+    p.eps = d.eps;
+    p.n_out = d.n_out;
+    // outputs in kernel order: softmax (which overwrites the row in
+    // registers) last; the order of independent outputs changes no bits
+    int order[kMaxFanOut], n_soft = 0, j = 0;
+    for (int i = 0; i < d.n_out; ++i)
+        if (d.out[i].op != kFanSoftmax) order[j++] = i;
+    for (int i = 0; i < d.n_out; ++i)
+        if (d.out[i].op == kFanSoftmax) {
+            order[j++] = i;
+            ++n_soft;
+        }
+    if (n_soft > 1) throw std::runtime_error("fan-out: at most one softmax output");
+    for (int i = 0; i < d.n_out; ++i) p.states[i] = d.states[i];
+    for (int jj = 0; jj < d.n_out; ++jj) {
+        const int i = order[jj];
+        const FanOutDesc &o = d.out[i];
+        CheckAligned(o.y, "fan-out y");
+        const bool ew = o.op == kEwGelu || o.op == kEwSilu || o.op == kEwCast;
+        if (!ew && o.op != kFanSoftmax && o.op != kFanRmsNorm) throw std::runtime_error("fan-out: unsupported op");
+        if (o.op != kEwCast && o.dtype != d.dtype_in) throw std::runtime_error("fan-out: only cast changes dtype");
+        if (o.op == kFanRmsNorm) CheckAligned(o.gamma, "fan-out gamma");
+        p.out[jj] = {o.op, o.dtype, o.y, static_cast<const uint16_t *>(o.gamma)};
+    }
+    if (d.wait.ctrl != nullptr && d.states[0] != d.wait.state0)
+        throw std::runtime_error("fan-out: states[0] must be the wait's state block");
+    p.tile_rows = d.tile_rows > 0 ? d.tile_rows : d.rows;
+    p.n_tiles = TileCount(d.rows, p.tile_rows);
+    p.w = d.wait;
+    const int chunks = d.cols / 8;
+    const int lpr = RowLanes(chunks);
+    int cpl = (chunks + lpr - 1) / lpr;
+    cpl = cpl <= 1 ? 1 : (cpl <= 2 ? 2 : (cpl <= 4 ? 4 : 8));
+    const int rpb = kThreads / lpr;
+    int grid = d.grid;
+    if (grid <= 0) grid = std::max(1, std::min((p.tile_rows + rpb - 1) / rpb, 8192));
+    if (d.dtype_in == kBF16) FanDispatch<kBF16>(p, lpr, cpl, grid, stream);
+    else FanDispatch<kF16>(p, lpr, cpl, grid, stream);
+    Check(hipGetLastError(), "fan-out launch");
+}
+
+void WaitLaunchMulti(const RelayWait &w, int lo, int hi, const int32_t *states, int n, hipStream_t stream)
+{
+    if (w.ctrl == nullptr) return;
+    if (n < 1 || n > kMaxFanOut) throw std::runtime_error("wait: 1..4 consumer states");
+    if (states[0] != w.state0) throw std::runtime_error("wait: states[0] must be the wait's state block");
+    WaitStates st{};
+    for (int i = 0; i < n; ++i) st.s[i] = states[i];
+    st.n = n;
+    hipLaunchKernelGGL(WaitMultiKernel, dim3(1), dim3(64), 0, stream, w, lo, hi, st);
+    Check(hipGetLastError(), "wait launch");
 }
 
 void WaitLaunch(const RelayWait &w, int lo, int hi, hipStream_t stream)

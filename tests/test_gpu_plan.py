@@ -147,3 +147,36 @@ def test_qwen_consumers_as_dag(gpu, tmp_path):
     for k in base:
         assert np.array_equal(base[k], outs[k]), k
     assert_close_to_oracle(schedule.serial_schedule(dag), outs)
+
+
+@pytest.mark.parametrize("k", [1, 4])
+def test_fanout_b0_and_uncoalesced_match_serial(gpu, tmp_path, k):
+    """B0 (two streams, unsplit) and the split run one launch per task
+    (KR_PLAN_COALESCE=0, the reference's task granularity) give the serial
+    bits, as the coalesced relay launches do."""
+    dag = workloads.mm_fanout(tmp_path, M=1024, K=512, N=2048)
+    _, base = run(schedule.serial_schedule(dag), tmp_path, "serial", iters=1, warmup=0)
+    v = workloads.variants(dag, k)
+    for name, sched, env in (("b0", v["b0"], None), ("split_nc", v["split"], {"KR_PLAN_COALESCE": "0"}),
+                             ("split_nofan", v["split"], {"KR_PLAN_FAN": "1"})):
+        r, outs = run(sched, tmp_path, "%s%d" % (name, k), mode="graph_per_stream", env=env)
+        assert r["ok"] and r["gate_timeouts"] == 0, (name, r)
+        for node in base:
+            assert np.array_equal(base[node], outs[node]), (name, k, node)
+
+
+def test_fused_fanout_all_ops(gpu, tmp_path):
+    """Four sibling consumers fused into one pass (rmsnorm, silu, cast to fp32,
+    softmax) behind a GEMM released in 4 row tiles: each output equals its
+    standalone kernel's bits and the oracle."""
+    inputs = workloads.write_inputs(tmp_path, 512, 256, 1024)
+    raw = workloads.mm_consumers_dag("fan4", 512, 256, 1024, ["rmsnorm", "silu", "cast", "softmax"],
+                                     inputs=inputs, cast_to="fp32")
+    dag = schedule.dag_from_dict(raw)
+    _, base = run(schedule.serial_schedule(dag), tmp_path, "serial")
+    for k in (1, 2, 4):
+        r, outs = run(workloads.variants(dag, k)["split"], tmp_path, "split%d" % k, mode="graph_per_stream")
+        assert r["ok"] and r["gate_timeouts"] == 0 and r["flag_edges"] == 4 * k, r
+        for node in base:
+            assert np.array_equal(base[node], outs[node]), (k, node)
+    assert_close_to_oracle(schedule.serial_schedule(dag), outs)
