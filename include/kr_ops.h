@@ -101,6 +101,17 @@ int kr_op_gemm_swiglu(int dtype, const void *A, int64_t lda, const void *Bt, int
                       void *act, int M, int cols, int K, const kr_pub *pub, int tail_tiles,
                       int order_rows, void *stream);
 
+/* Gate/up GEMM with SwiGLU applied in its epilogue (the relay of
+ * matmul_gate/up -> Silu -> Mul at MFMA-tile granularity, handed over in
+ * registers): for A[M,K] . Bt[2*cols,K]^T with gate/up interleaved in groups
+ * of 8 columns, writes act[M, cols] (row stride ld_act) =
+ * bf16(bf16(silu(gate)) * up) with the rounding of kr_op_elementwise's
+ * swiglu_gu over the stored product; the [M, 2*cols] product itself is not
+ * written. cols must be a multiple of 8. Replaces the same reference call
+ * sites as kr_op_gemm_swiglu (exec/qwen_main.cpp:616-644, 888-889). */
+int kr_op_gemm_swiglu_epilogue(int dtype, const void *A, int64_t lda, const void *Bt, int64_t ldb, void *act,
+                               int64_t ld_act, int M, int cols, int K, void *stream);
+
 /* Elementwise op on [rows, cols]; x1 used by mul/add/swiglu; dtype_out
  * differs from dtype_in only for cast. tile_rows = relay granularity
  * (0 = rows); grid = workgroups (0 = sized to the tensor). wait/pub may be

@@ -29,6 +29,12 @@ struct GemmDesc {
     bool coresident = false;     // a consumer kernel spins on the same CUs while
                                  // this GEMM runs: use a tile whose workgroup
                                  // leaves register room beside it (not 256x256)
+    // SwiGLU epilogue (the in-register relay of gate/up to its consumer):
+    // C's columns are gate/up interleaved in groups of 8; instead of C the
+    // launch writes epi_act[M, N/2] (row stride ld_act) = bf16(silu(gate))*up,
+    // rounded as the standalone SwiGLU kernel rounds. C is not written.
+    void *epi_act = nullptr;
+    int64_t ld_act = 0;
     int order_rows = 0;          // > 0: produce in runs of this many rows (a
                                  // multiple of pub.rows_per_tile), default
                                  // one run per relay tile

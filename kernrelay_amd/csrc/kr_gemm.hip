@@ -51,6 +51,8 @@ struct GemmParams {
     RelayWait wait;
     uint16_t *tail_act;  // SwiGLU tail consumer output (nullptr: none)
     int tail_cols;
+    uint16_t *epi_act;   // SwiGLU epilogue output [M, N/2] (nullptr: store C)
+    int64_t ld_act;
     int gemm_wgs;        // workgroups of the GEMM proper; the rest are tail
     int tail_wpt;        // tail workgroups per relay tile
 };
@@ -255,6 +257,61 @@ __device__ __forceinline__ void StoreTile(const GemmParams &p, f32x16 (&acc)[MI]
     }
 }
 
+// SwiGLU epilogue: the in-register relay of the gate/up GEMM to its
+// consumer. C's columns hold gate and up interleaved in groups of 8 (cols
+// 16q..16q+7 gate, 16q+8..16q+15 up), so in each 32x32 C^T block a lane's
+// values v = 0..3 are gate columns 8g'+4h+e of group q (g' = 2q) and v = 4..7
+// the matching up columns (g' = 2q + 1): act[row, 8q + 4h + e] =
+// bf16(bf16(silu(bf16(gate))) * bf16(up)), the rounding of the standalone
+// SwiGLU kernel reading the stored gate/up tile. C itself is not written.
+// The BM x BN/2 act tile is staged in LDS like StoreTile's and leaves as
+// full-line 16-byte stores.
+template <int DT, int BM, int BN, int MI, int NI>
+__device__ __forceinline__ void StoreTileSwiglu(const GemmParams &p, f32x16 (&acc)[MI][NI], uint16_t *stage, int m0,
+                                                int n0, int wm, int wn, int lane)
+{
+    constexpr int AW = BN / 2;  // act columns of the tile
+    static_assert(AW >= 128, "slot swizzle needs >= 32 slots per row");
+    const int lrow = lane & 31;
+    const int lhalf = lane >> 5;
+#pragma unroll
+    for (int j = 0; j < NI; ++j) {
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+            const int acol = wn * (AW / 2) + j * 16 + q * 8 + 4 * lhalf;
+#pragma unroll
+            for (int i = 0; i < MI; ++i) {
+                const int row = wm * (BM / 2) + i * 32 + lrow;
+                uint32_t h[4];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const float g = RoundTo<DT>(acc[i][j][8 * q + e]);
+                    const float u = RoundTo<DT>(acc[i][j][8 * q + 4 + e]);
+                    h[e] = Elem<DT>::Store(RoundTo<DT>(Silu(g)) * u);
+                }
+                const int slot = (acol >> 2) ^ (row & 31);
+                *reinterpret_cast<uint2 *>(stage + row * AW + slot * 4) =
+                    make_uint2(h[0] | (h[1] << 16), h[2] | (h[3] << 16));
+            }
+        }
+    }
+    __syncthreads();
+    constexpr int CPR = AW / 8;
+    const int64_t a0 = n0 / 2;
+    const int acols = p.N / 2;
+#pragma unroll 4
+    for (int idx = threadIdx.x; idx < BM * CPR; idx += kThreads) {
+        const int row = idx / CPR;
+        const int ch = idx % CPR;
+        const int gm = m0 + row;
+        const int gn = int(a0) + ch * 8;
+        if (gm >= p.M || gn >= acols) continue;
+        uint4 v = *reinterpret_cast<const uint4 *>(stage + row * AW + (ch ^ ((row & 31) >> 1)) * 8);
+        if (row & 1) v = make_uint4(v.z, v.w, v.x, v.y);
+        PutU128(p.epi_act + int64_t(gm) * p.ld_act + gn, v, p.store_kind == 0 || p.pub.ctrl != nullptr);
+    }
+}
+
 template <int DT, int BM, int BN>
 __global__ void __attribute__((amdgpu_flat_work_group_size(kThreads, kThreads),
                                amdgpu_waves_per_eu(BM * BN >= 256 * 128 ? 1 : 2, BM * BN >= 256 * 128 ? 1 : 2)))
@@ -373,7 +430,15 @@ GemmKernel(GemmParams p)
         __syncthreads();
     }
 
-    StoreTile<DT, BM, BN>(p, acc, smem, m0, n0, wm, wn, lane);
+    if constexpr (BN >= 256) {
+        if (p.epi_act != nullptr) {
+            StoreTileSwiglu<DT, BM, BN>(p, acc, smem, m0, n0, wm, wn, lane);
+        } else {
+            StoreTile<DT, BM, BN>(p, acc, smem, m0, n0, wm, wn, lane);
+        }
+    } else {
+        StoreTile<DT, BM, BN>(p, acc, smem, m0, n0, wm, wn, lane);
+    }
     if (p.pub.ctrl != nullptr) RelayArrive(p.pub, m0 / p.pub.rows_per_tile);
     RelayFinish(p.wait);
 }
@@ -511,6 +576,15 @@ void GemmLaunch(const GemmDesc &d, hipStream_t stream)
     p.store_kind = StoreKind();
     p.tail_act = static_cast<uint16_t *>(d.tail_act);
     p.tail_cols = d.tail_cols;
+    p.epi_act = static_cast<uint16_t *>(d.epi_act);
+    p.ld_act = d.ld_act;
+    if (p.epi_act != nullptr) {
+        if (p.tail_act != nullptr) throw std::runtime_error("gemm: SwiGLU epilogue and tail consumer are exclusive");
+        if (d.dtype != kBF16 && d.dtype != kF16) throw std::runtime_error("gemm swiglu: 16-bit output only");
+        if (d.N % 16 != 0) throw std::runtime_error("gemm swiglu: N must be a multiple of 16 (gate/up groups of 8)");
+        if ((reinterpret_cast<uintptr_t>(d.epi_act) & 15) || d.ld_act % 8 != 0 || d.ld_act < d.N / 2)
+            throw std::runtime_error("gemm swiglu: act must be 16-byte aligned with ld_act >= N/2, a multiple of 8");
+    }
     if (p.tail_act != nullptr) {
         if (p.pub.ctrl == nullptr || d.M % p.pub.rows_per_tile != 0)
             throw std::runtime_error("gemm tail: needs a relay release over whole tiles of M");
@@ -536,6 +610,7 @@ void GemmLaunch(const GemmDesc &d, hipStream_t stream)
         t.bn = d.bn;
     }
     if (t.bm < 0) throw std::runtime_error("gemm: relay tile rows must be a multiple of 64");
+    if (d.epi_act != nullptr && t.bn < 256) t = {t.bm >= 256 ? 256 : 128, 256};  // the epilogue pairs 16-col groups
     const bool bf = d.dtype == kBF16;
     if (d.dtype != kBF16 && d.dtype != kF16) throw std::runtime_error("gemm: dtype must be bf16 or f16");
     const int order = d.order_rows;

@@ -116,6 +116,27 @@ int kr_op_gemm_swiglu(int dtype, const void *A, int64_t lda, const void *Bt, int
     });
 }
 
+int kr_op_gemm_swiglu_epilogue(int dtype, const void *A, int64_t lda, const void *Bt, int64_t ldb, void *act,
+                               int64_t ld_act, int M, int cols, int K, void *stream)
+{
+    return Guard([&] {
+        kr::GemmDesc d;
+        d.dtype = dtype;
+        d.A = A;
+        d.Bt = Bt;
+        d.C = nullptr;
+        d.lda = lda;
+        d.ldb = ldb;
+        d.ldc = 2 * int64_t(cols);
+        d.M = M;
+        d.N = 2 * cols;
+        d.K = K;
+        d.epi_act = act;
+        d.ld_act = ld_act;
+        kr::GemmLaunch(d, S(stream));
+    });
+}
+
 int kr_op_elementwise(int op, int dtype_in, int dtype_out, const void *x0, const void *x1, void *y, int rows,
                       int cols, int tile_rows, int grid, const kr_wait *wait, const kr_pub *pub, void *stream)
 {

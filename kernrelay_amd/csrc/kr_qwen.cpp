@@ -713,32 +713,36 @@ private:
         });
     }
 
-    // relay_split[:k] — the relay on MI355X. The gate/up GEMM releases its k
-    // row tiles through the flags as they complete, and the SwiGLU consumer
-    // starts on released tiles inside the same launch: its workgroups are
-    // appended to the GEMM's grid, so the dispatcher hands them out only as
-    // the GEMM's last round frees CUs, which the serial schedule leaves idle
-    // (that round is 1184 mod 256 = 160 of 256 CUs for the 7B layer). The
-    // appended consumer takes the tiles released before that round; the
-    // tiles released at the very end are run at full width right after the
-    // GEMM. Producing row tile by row tile makes every run re-read the whole
-    // weight, so with k >= 4 the GEMM produces in halves (tiles 0..k/2-1 are
-    // released together mid-GEMM) — KR_SPLIT_ORDER_ROWS / KR_SPLIT_TAIL_TILES
-    // override both. The
-    // consumer is not given a CU partition of its own: measured on MI355X, a
-    // static partition costs every producer kernel its CUs (5.5% of the
-    // prefill for 2 CUs per XCD) and consumer workgroups interleaved onto the
-    // producer's CUs starve 256x256 GEMM workgroups, which need a whole CU.
-    // Edges behind single-wave producers (o, down -> Add+RMSNorm) release all
-    // their tiles at once, so they stay in stream order. Every row goes
-    // through the same arithmetic as in the serial schedule: identical bits.
+    // relay_split[:k] — the relay on MI355X. By default the gate/up GEMM
+    // hands every finished MFMA tile to its SwiGLU consumer in registers (the
+    // epilogue computes act from the tile's interleaved gate/up pairs with the
+    // rounding of the standalone kernel): the consumer starts on each tile the
+    // moment it exists, and the [S, 2I] gate/up product never goes to HBM.
+    // With KR_SPLIT_SWIGLU=flags the GEMM instead releases its k row tiles
+    // through the flags, and SwiGLU workgroups appended to the GEMM's grid
+    // start on each released tile as the GEMM's last round frees CUs (that
+    // round is 1184 mod 256 = 160 of 256 CUs for the 7B layer); tiles released
+    // at the very end run at full width right after the GEMM, and with k >= 4
+    // the GEMM produces in halves (producing tile by tile makes every run
+    // re-read the whole weight) — KR_SPLIT_ORDER_ROWS / KR_SPLIT_TAIL_TILES
+    // override both. Measured on MI355X, a static CU partition for the
+    // consumer costs every producer kernel its CUs (5.5% of the prefill for 2
+    // CUs per XCD), and consumer workgroups interleaved onto the producer's
+    // CUs starve 256x256 GEMM workgroups, which need a whole CU. Edges behind
+    // single-round producers (o, down -> Add+RMSNorm) release all their tiles
+    // at once, so they stay in stream order. Every row goes through the same
+    // arithmetic as in the serial schedule: identical bits.
     void BuildSplit()
     {
         const int S = seq_;
         const int k = mode_.tiles;
         const int T = S / k;
         const int P = 0;
-        const int gu_act = NewEdge(k * L_);  // block (l, t) = gu_act + l*k + t
+        // SwiGLU: in the gate/up GEMM's epilogue (default), or a consumer
+        // appended to its launch waiting on its k released row tiles
+        // (KR_SPLIT_SWIGLU=flags)
+        const bool swiglu_epi = EnvStr("KR_SPLIT_SWIGLU", "epilogue") != "flags";
+        const int gu_act = swiglu_epi ? 0 : NewEdge(k * L_);  // block (l, t) = gu_act + l*k + t
         const int order_rows = EnvInt("KR_SPLIT_ORDER_ROWS", k >= 4 ? S / 2 : T);
         const int tail_tiles = std::max(0, std::min(k, EnvInt("KR_SPLIT_TAIL_TILES", k >= 4 ? k / 2 : k - 1)));
         if (order_rows <= 0 || order_rows % T != 0 || S % order_rows != 0)
@@ -763,7 +767,24 @@ private:
             EmitAttention(P, l, RelayWait{});
             Gemm(P, attn_.get(), int64_t(HQ_) * D_, w.o, H_, HQ_ * D_, o_.get(), H_, nullptr, S, RelayPub{});
             AddRmsNorm(P, hcur, o_.get(), w.ln2, x, hnxt, RelayWait{}, 0, RelayPub{}, 0);
-            {
+            if (swiglu_epi) {
+                // gate/up with SwiGLU in its epilogue: each MFMA tile hands
+                // its gate/up pairs to the consumer in registers and only act
+                // is written
+                GemmDesc d;
+                d.dtype = kBF16;
+                d.A = x;
+                d.lda = H_;
+                d.Bt = w.gu;
+                d.ldb = H_;
+                d.ldc = 2 * int64_t(I_);
+                d.M = S;
+                d.N = 2 * I_;
+                d.K = H_;
+                d.epi_act = act_.get();
+                d.ld_act = I_;
+                Timed(P, [&] { Emit(P, [d](hipStream_t st) { GemmLaunch(d, st); }); });
+            } else {
                 // gate/up, its k released tiles consumed by the appended SwiGLU
                 GemmDesc d;
                 d.dtype = kBF16;

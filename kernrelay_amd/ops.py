@@ -51,11 +51,12 @@ def _lib():
         L.kr_op_transpose.argtypes = [vp, vp, i32, i32, vp]
         L.kr_op_gemm_swiglu.argtypes = [i32, vp, i64, vp, i64, vp, vp, i32, i32, i32, ctypes.POINTER(KrPub),
                                         i32, i32, vp]
+        L.kr_op_gemm_swiglu_epilogue.argtypes = [i32, vp, i64, vp, i64, vp, i64, i32, i32, i32, vp]
         L.kr_op_stream_create.argtypes = []
         L.kr_op_stream_create.restype = vp
         L.kr_op_stream_destroy.argtypes = [vp]
         L.kr_op_stream_destroy.restype = ctypes.c_int
-        for name in ("kr_op_gemm", "kr_op_gemm_swiglu", "kr_op_elementwise", "kr_op_rowop", "kr_op_wait", "kr_op_publish",
+        for name in ("kr_op_gemm", "kr_op_gemm_swiglu", "kr_op_gemm_swiglu_epilogue", "kr_op_elementwise", "kr_op_rowop", "kr_op_wait", "kr_op_publish",
                      "kr_op_embedding", "kr_op_rope", "kr_op_attention", "kr_op_transpose"):
             getattr(L, name).restype = ctypes.c_int
         _BOUND = True
@@ -138,6 +139,17 @@ def gemm_swiglu(A, Bt, C, act, pub, tail_tiles=0, order_rows=0, stream=None):
     assert Bt.shape == (2 * cols, K) and C.shape == (M, 2 * cols) and act.shape[0] == M
     _check(_lib().kr_op_gemm_swiglu(_dt(A), _ptr(A), A.stride(0), _ptr(Bt), Bt.stride(0), _ptr(C), _ptr(act),
                                     M, cols, K, ctypes.byref(pub), tail_tiles, order_rows, _stream(stream)))
+
+
+def gemm_swiglu_epilogue(A, Bt, act, stream=None):
+    """act[M, I] = SwiGLU of A @ Bt^T (Bt = [2I, K], gate/up interleaved in
+    groups of 8 rows), applied in the GEMM's epilogue; the product itself is
+    never written."""
+    M, K = A.shape
+    cols = act.shape[1]
+    assert Bt.shape == (2 * cols, K) and act.shape[0] == M
+    _check(_lib().kr_op_gemm_swiglu_epilogue(_dt(A), _ptr(A), A.stride(0), _ptr(Bt), Bt.stride(0), _ptr(act),
+                                             act.stride(0), M, cols, K, _stream(stream)))
 
 
 def elementwise(op, x0, y, x1=None, rows=None, cols=None, tile_rows=0, grid=0, wait=None, pub=None,

@@ -375,3 +375,32 @@ def test_relay_wait_bound_reports_timeout(gpu):
     torch.cuda.synchronize()
     blk = ctrl.cpu().reshape(2, ops.CTRL_WORDS)
     assert int(blk[0, 2]) == 1 and int(blk[0, 1]) == 2 and int(blk[0, 0]) == 2
+
+
+@pytest.mark.parametrize("M,I,K", [(1024, 1536, 512), (300, 512, 256), (2048, 4864, 896)])
+def test_gemm_swiglu_epilogue_bit_exact(gpu, M, I, K):
+    """SwiGLU applied in the gate/up GEMM's epilogue (the in-register relay)
+    equals the GEMM followed by the standalone swiglu_gu kernel bit for bit
+    (ragged M included) and writes nothing outside act; the product and its
+    SwiGLU each match the oracle."""
+    announce("gemm swiglu epilogue %dx%dx%d" % (M, I, K))
+    A = rand((M, K), 1.0, 40).cuda()
+    Bt = rand((2 * I, K), 0.05, 41).cuda()
+    ref_c = torch.empty(M, 2 * I, dtype=torch.bfloat16, device="cuda")
+    ref_a = torch.empty(M, I, dtype=torch.bfloat16, device="cuda")
+    ops.gemm(A, Bt, ref_c)
+    ops.elementwise("swiglu_gu", ref_c, ref_a, rows=M, cols=I)
+    pad = torch.full((M + 8, I + 16), 7.0, dtype=torch.bfloat16, device="cuda")
+    act = pad[:M, :I]
+    for _ in range(2):
+        act.zero_()
+        ops.gemm_swiglu_epilogue(A, Bt, act)
+        torch.cuda.synchronize()
+        assert torch.equal(act, ref_a)
+    assert torch.all(pad[M:] == 7.0) and torch.all(pad[:, I:] == 7.0)
+    # each stage against the oracle at its own tolerance: the product, then
+    # SwiGLU of that product (four bf16 roundings in a row turn a one-ulp
+    # difference of the fp32 sum order into several ulps of act)
+    close(ref_c, O.gemm(A.cpu(), Bt.cpu().t()))
+    g = ref_c.cpu().view(M, I // 8, 2, 8)
+    close(act, O.swiglu(g[:, :, 0, :].reshape(M, I), g[:, :, 1, :].reshape(M, I)))

@@ -65,7 +65,8 @@ def test_all_modes_bit_exact_and_match_oracle(gpu, tmp_path, preset):
 
 def test_qwen05_shapes_split_bit_exact(gpu, tmp_path):
     """Qwen2.5-0.5B layer shapes (H 896, 14/2 heads, D 64, I 4864, V 151936,
-    tied) at seq 2048, two layers: serial == relay_split:4, oracle argmax."""
+    tied) at seq 2048, two layers: serial == relay_split:4 (SwiGLU in the
+    gate/up epilogue, and flag-released), oracle argmax."""
     seq = 2048
     d, ref = make(tmp_path, "qwen2.5-0.5b", seq, layers=2)
     dump = tmp_path / "dump"
@@ -74,7 +75,16 @@ def test_qwen05_shapes_split_bit_exact(gpu, tmp_path):
     check_logits(dump, ref)
     b = run(d, "relay_split:4", seq)
     assert a["logits_fnv64"] == b["logits_fnv64"]
-    assert b["flag_timeouts"] == 0 and b["flag_edges"] > 0
+    assert b["flag_timeouts"] == 0
+    # the flag-released variant: SwiGLU workgroups appended to the gate/up
+    # GEMM wait on its 4 row tiles
+    os.environ["KR_SPLIT_SWIGLU"] = "flags"
+    try:
+        c = run(d, "relay_split:4", seq)
+    finally:
+        del os.environ["KR_SPLIT_SWIGLU"]
+    assert a["logits_fnv64"] == c["logits_fnv64"]
+    assert c["flag_timeouts"] == 0 and c["flag_edges"] > 0
 
 
 def test_profile_many(gpu, tmp_path):
