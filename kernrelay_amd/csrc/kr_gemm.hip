@@ -5,8 +5,9 @@
 // Bt = weight_t^T ([N,K], K contiguous) so that both operands feed
 // v_mfma_f32_32x32x16_{bf16,f16} with one 16-byte load per lane.
 //
-// * 256 threads = 4 waves in a 2x2 grid; each wave owns (BM/2)x(BN/2) of C as
-//   (BM/64)x(BN/64) 32x32 accumulator blocks (fp32, 16 values per lane).
+// * 4 waves in a 2x2 grid (each wave owns (BM/2)x(BN/2) of C), or for
+//   256x256 tiles 8 waves in a 2x4 grid (128x64 each, two waves per SIMD), as
+//   32x32 accumulator blocks (fp32, 16 values per lane).
 // * K is walked in 64-wide steps through a double-buffered LDS stage; global
 //   loads of step k+1 are in flight while step k runs on the matrix cores.
 // * LDS rows are 128 B (64 elements); the 16-byte chunk index is XOR-swizzled
@@ -46,6 +47,7 @@ struct GemmParams {
     int M, N, K;
     int tiles_m, tiles_n;
     int order_rows;  // > 0: dispatch tiles in relay-tile order, this many rows each
+    int group_m;     // raster: row blocks per group (0 = all)
     int store_kind;  // 0 device-scope (default), 1 plain, 2 nontemporal
     RelayPub pub;
     RelayWait wait;
@@ -62,15 +64,18 @@ __device__ __forceinline__ int Swz(int row, int chunk) { return chunk ^ ((row >>
 // Workgroup -> output tile. The dispatcher deals workgroups to the 8 XCDs
 // round-robin (XCD = blockIdx % 8) and each XCD has its own L2. Within a run
 // of `per` consecutive workgroup ids starting at `first`, XCD x takes a
-// contiguous chunk of the run's tiles (row blocks fastest), so a weight column
-// block is read by workgroups of one XCD while it sits in that XCD's L2.
-// * No relay: one run over all tiles.
+// contiguous chunk of the run's tiles, so a weight column block is read by
+// workgroups of one XCD while it sits in that XCD's L2.
+// * No relay: one run over all tiles, rastered in groups of group_m row
+//   blocks (row blocks fastest within a group), so the tiles an XCD runs at
+//   once form a near-square patch of C.
 // * Relay (order_rows > 0): one run per relay tile, front to back, so tile 0
 //   of the rows is complete first; each run covers order_rows/bm row blocks,
 //   odd runs with the weight columns in reverse (each run reads all of the
 //   weight, and the blocks the last run read are the ones still cached).
 
-__device__ __forceinline__ void TileOf(int bid, int tiles_m, int tiles_n, int bm, int order_rows, int &tm, int &tn)
+__device__ __forceinline__ void TileOf(int bid, int tiles_m, int tiles_n, int bm, int order_rows, int group_m, int &tm,
+                                       int &tn)
 {
     if (order_rows > 0) {
         const int mt = order_rows / bm;  // row blocks per relay tile
@@ -84,9 +89,18 @@ __device__ __forceinline__ void TileOf(int bid, int tiles_m, int tiles_n, int bm
         if (r & 1) tn = tiles_n - 1 - tn;
         return;
     }
+    // grouped raster: runs of `group_m` row blocks fastest, so an XCD's
+    // concurrent tiles form a near-square patch (fewer distinct operand
+    // slices per K stage in its L2) rather than a tall column
     const int t = XcdChunk(bid, 0, tiles_m * tiles_n);
-    tm = t % tiles_m;
-    tn = t / tiles_m;
+    const int gm_all = group_m > 0 ? min(group_m, tiles_m) : tiles_m;
+    const int per_group = gm_all * tiles_n;
+    const int g = t / per_group;
+    const int first_m = g * gm_all;
+    const int gm = min(tiles_m - first_m, gm_all);
+    const int r = t - g * per_group;
+    tm = first_m + r % gm;
+    tn = r / gm;
 }
 
 template <int DT>
@@ -155,8 +169,8 @@ __device__ void TailSwiglu(const GemmParams &p)
     const int64_t chunks = rows * p.tail_cols / 8;
     const uint16_t *src = p.C + int64_t(t) * rows * p.ldc;
     uint16_t *dst = p.tail_act + int64_t(t) * rows * p.tail_cols;
-    const int64_t stride = int64_t(p.tail_wpt) * kThreads;
-    int64_t c = int64_t(w) * kThreads + threadIdx.x;
+    const int64_t stride = int64_t(p.tail_wpt) * blockDim.x;
+    int64_t c = int64_t(w) * blockDim.x + threadIdx.x;
     for (; c + 3 * stride < chunks; c += 4 * stride) {
         GemmU32x4 g[4], u[4];
         LoadGateUp4(src + c * 16, src + (c + stride) * 16, src + (c + 2 * stride) * 16, src + (c + 3 * stride) * 16, g,
@@ -191,10 +205,11 @@ __device__ void TailSwiglu(const GemmParams &p)
 // with device-scope stores when the launch releases relay tiles.
 // `stage` must hold BM*BN 16-bit values and be free (all waves past their
 // last LDS read of the main loop).
-template <int DT, int BM, int BN, int MI, int NI>
+template <int DT, int BM, int BN, int NT, int MI, int NI>
 __device__ __forceinline__ void StoreTile(const GemmParams &p, f32x16 (&acc)[MI][NI], uint16_t *stage, int m0,
                                           int n0, int wm, int wn, int lane)
 {
+    constexpr int WTN = NI * 32;  // columns per wave
     static_assert(BN >= 128, "slot swizzle needs >= 32 slots per row");
     const int lrow = lane & 31;
     const int lhalf = lane >> 5;
@@ -202,7 +217,7 @@ __device__ __forceinline__ void StoreTile(const GemmParams &p, f32x16 (&acc)[MI]
     for (int j = 0; j < NI; ++j) {
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
-            const int col = wn * (BN / 2) + j * 32 + 8 * g + 4 * lhalf;
+            const int col = wn * WTN + j * 32 + 8 * g + 4 * lhalf;
             float b[4] = {0.0f, 0.0f, 0.0f, 0.0f};
             if (p.bias != nullptr) {
 #pragma unroll
@@ -233,7 +248,7 @@ __device__ __forceinline__ void StoreTile(const GemmParams &p, f32x16 (&acc)[MI]
     // (KR_GEMM_STORE=plain|nt for comparison)
     const bool coh = p.store_kind == 0 || p.pub.ctrl != nullptr;
 #pragma unroll 4
-    for (int idx = threadIdx.x; idx < BM * CPR; idx += kThreads) {
+    for (int idx = threadIdx.x; idx < BM * CPR; idx += NT) {
         const int row = idx / CPR;
         const int ch = idx % CPR;
         const int gm = m0 + row;
@@ -266,11 +281,12 @@ __device__ __forceinline__ void StoreTile(const GemmParams &p, f32x16 (&acc)[MI]
 // SwiGLU kernel reading the stored gate/up tile. C itself is not written.
 // The BM x BN/2 act tile is staged in LDS like StoreTile's and leaves as
 // full-line 16-byte stores.
-template <int DT, int BM, int BN, int MI, int NI>
+template <int DT, int BM, int BN, int NT, int MI, int NI>
 __device__ __forceinline__ void StoreTileSwiglu(const GemmParams &p, f32x16 (&acc)[MI][NI], uint16_t *stage, int m0,
                                                 int n0, int wm, int wn, int lane)
 {
     constexpr int AW = BN / 2;  // act columns of the tile
+    constexpr int WTA = NI * 16;  // act columns per wave
     static_assert(AW >= 128, "slot swizzle needs >= 32 slots per row");
     const int lrow = lane & 31;
     const int lhalf = lane >> 5;
@@ -278,7 +294,7 @@ __device__ __forceinline__ void StoreTileSwiglu(const GemmParams &p, f32x16 (&ac
     for (int j = 0; j < NI; ++j) {
 #pragma unroll
         for (int q = 0; q < 2; ++q) {
-            const int acol = wn * (AW / 2) + j * 16 + q * 8 + 4 * lhalf;
+            const int acol = wn * WTA + j * 16 + q * 8 + 4 * lhalf;
 #pragma unroll
             for (int i = 0; i < MI; ++i) {
                 const int row = wm * (BM / 2) + i * 32 + lrow;
@@ -300,7 +316,7 @@ __device__ __forceinline__ void StoreTileSwiglu(const GemmParams &p, f32x16 (&ac
     const int64_t a0 = n0 / 2;
     const int acols = p.N / 2;
 #pragma unroll 4
-    for (int idx = threadIdx.x; idx < BM * CPR; idx += kThreads) {
+    for (int idx = threadIdx.x; idx < BM * CPR; idx += NT) {
         const int row = idx / CPR;
         const int ch = idx % CPR;
         const int gm = m0 + row;
@@ -336,7 +352,7 @@ GemmKernel(GemmParams p)
     const int wn = wave & 1;
 
     int tm, tn;
-    TileOf(blockIdx.x, p.tiles_m, p.tiles_n, BM, p.order_rows, tm, tn);
+    TileOf(blockIdx.x, p.tiles_m, p.tiles_n, BM, p.order_rows, p.group_m, tm, tn);
     const int m0 = tm * BM;
     const int n0 = tn * BN;
     RelayWaitRows(p.wait, m0, min(m0 + BM, p.M));
@@ -432,12 +448,12 @@ GemmKernel(GemmParams p)
 
     if constexpr (BN >= 256) {
         if (p.epi_act != nullptr) {
-            StoreTileSwiglu<DT, BM, BN>(p, acc, smem, m0, n0, wm, wn, lane);
+            StoreTileSwiglu<DT, BM, BN, kThreads>(p, acc, smem, m0, n0, wm, wn, lane);
         } else {
-            StoreTile<DT, BM, BN>(p, acc, smem, m0, n0, wm, wn, lane);
+            StoreTile<DT, BM, BN, kThreads>(p, acc, smem, m0, n0, wm, wn, lane);
         }
     } else {
-        StoreTile<DT, BM, BN>(p, acc, smem, m0, n0, wm, wn, lane);
+        StoreTile<DT, BM, BN, kThreads>(p, acc, smem, m0, n0, wm, wn, lane);
     }
     if (p.pub.ctrl != nullptr) RelayArrive(p.pub, m0 / p.pub.rows_per_tile);
     RelayFinish(p.wait);
@@ -463,6 +479,31 @@ int StoreKind()
         const char *e = std::getenv("KR_GEMM_STORE");
         if (e == nullptr) return 0;
         return std::string(e) == "plain" ? 1 : std::string(e) == "nt" ? 2 : 0;
+    }();
+    return v;
+}
+
+// Row blocks per raster group of a launch without relay order
+// (KR_GEMM_GROUP_M, default 4; 0 = all rows, a column at a time); it changes
+// timing only, never the bits.
+int RasterGroupM()
+{
+    static const int v = [] {
+        const char *e = std::getenv("KR_GEMM_GROUP_M");
+        return e != nullptr ? std::max(0, std::atoi(e)) : 4;
+    }();
+    return v;
+}
+
+// Waves per workgroup of the 256x256 pipelined kernel (KR_GEMM_WAVES: 8
+// default, two per SIMD; 4 = one per SIMD); it changes timing only, never
+// the bits. Measured on MI355X (cold operands): 4096^3 138 -> 130 us, the
+// 2048x4608x3584 QKV 112 -> 104 us, lm_head 2068 -> 2036 us.
+int PipeWaves()
+{
+    static const int v = [] {
+        const char *e = std::getenv("KR_GEMM_WAVES");
+        return e != nullptr && std::atoi(e) == 4 ? 4 : 8;
     }();
     return v;
 }
@@ -500,6 +541,7 @@ void LaunchTyped(const GemmParams &base, int order_rows, int tail_tiles, hipStre
         p.order_rows = p.wait.prod_rows;  // the rows that are released first run first
     }
     p.gemm_wgs = p.tiles_m * p.tiles_n;
+    p.group_m = RasterGroupM();
     int grid_x = p.gemm_wgs;
     if (p.tail_act != nullptr) {
         p.tail_wpt = 256;  // one per CU of the device: enough to fill the idle CUs of the last round
@@ -507,10 +549,17 @@ void LaunchTyped(const GemmParams &base, int order_rows, int tail_tiles, hipStre
     }
     const dim3 grid(grid_x);
     if (p.K % kPipeK == 0 && !ForceSimple()) {
+        if constexpr (BM == 256 && BN == 256) {
+            if (PipeWaves() == 8) {
+                hipLaunchKernelGGL((GemmPipeKernel<DT, BM, BN, 0, 8>), grid, dim3(512), 0, stream, p);
+                Check(hipGetLastError(), "gemm launch");
+                return;
+            }
+        }
         switch (PrefetchStages()) {
-        case 2: hipLaunchKernelGGL((GemmPipeKernel<DT, BM, BN, 2>), grid, dim3(kThreads), 0, stream, p); break;
-        case 4: hipLaunchKernelGGL((GemmPipeKernel<DT, BM, BN, 4>), grid, dim3(kThreads), 0, stream, p); break;
-        default: hipLaunchKernelGGL((GemmPipeKernel<DT, BM, BN, 0>), grid, dim3(kThreads), 0, stream, p); break;
+        case 2: hipLaunchKernelGGL((GemmPipeKernel<DT, BM, BN, 2, 4>), grid, dim3(kThreads), 0, stream, p); break;
+        case 4: hipLaunchKernelGGL((GemmPipeKernel<DT, BM, BN, 4, 4>), grid, dim3(kThreads), 0, stream, p); break;
+        default: hipLaunchKernelGGL((GemmPipeKernel<DT, BM, BN, 0, 4>), grid, dim3(kThreads), 0, stream, p); break;
         }
     } else {
         hipLaunchKernelGGL((GemmKernel<DT, BM, BN>), grid, dim3(kThreads), 0, stream, p);
