@@ -32,30 +32,42 @@ def log(msg):
     print("[bench] " + msg, file=sys.stderr, flush=True)
 
 
-# HBM bytes per launch of the gate/up GEMM at 2048x37888x3584 (bf16), from
-# two rocprofv3 --pmc passes over one launch: FETCH_SIZE 437495 KiB x 2.0 +
-# WRITE_SIZE 151552 KiB x 1.0, the factors being what the same counters read
-# for a plain 512 MiB device copy (FETCH 262156 KiB, WRITE 524288 KiB).
-GATE_UP_TRAFFIC_BYTES = (437495 * 2.0 + 151552 * 1.0) * 1024
-GATE_UP_TRAFFIC_SOURCE = "profiles/gemm_gate_up_2048x37888x3584.md"
+# HBM bytes per launch of the gate/up GEMM with SwiGLU epilogue at
+# 2048x37888x3584 (bf16), from two rocprofv3 --pmc passes over single
+# launches (FETCH_SIZE, then WRITE_SIZE, KiB per dispatch), each scaled by
+# what the same counter reads for a plain 512 MiB device copy; and rocprof's
+# MFMA utilisation of the same launches (SQ_VALU_MFMA_BUSY_CYCLES over
+# GRBM_GUI_ACTIVE x SIMDs, at the clock the card ran).
+GATE_UP_TRAFFIC_BYTES = (408694.5 * 2.0 + 75776.0 * 1.0) * 1024
+GATE_UP_MFMA_UTIL = 0.573
+GATE_UP_TRAFFIC_SOURCE = "profiles/gemm_gate_up_swiglu_2048x37888x3584.md"
 
 
-def gemm_roofline(run, S, N, K):
-    """The dominant kernel, the gate/up GEMM, timed inside the prefill: with
-    KR_TIME_GATE_UP=1 the library runs one more pass of the same program after
-    the timed graph replays, launched eagerly with HIP events around each
-    gate/up launch on the stream it runs on, and reports their average (28
-    launches, interleaved with the layer's other kernels as in the timed
-    run)."""
+def gemm_roofline(run, serial, S, N, K):
+    """The dominant kernel of the measured (relay split) prefill: the gate/up
+    GEMM with SwiGLU in its epilogue. With KR_TIME_GATE_UP=1 the library runs
+    one more pass of the same program after the timed graph replays,
+    launched eagerly with HIP events around each gate/up launch on the
+    stream it runs on, and reports their average (28 launches, interleaved
+    with the layer's other kernels as in the timed run). Algorithmic work
+    2*S*N*K flop per launch; algorithmic bytes A + B + act (the epilogue
+    writes act[S, N/2], never the [S, N] product)."""
     avg_us = run["gate_up_avg_us"]
     flops = 2.0 * S * N * K
     achieved = flops / (avg_us * 1e-6) / 1e12
+    ser_us = serial["gate_up_avg_us"]
     return {"bound": "mfma", "achieved": round(achieved, 1), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
-            "frac": round(achieved / PEAK_BF16_TFLOPS, 4), "traffic": round(GATE_UP_TRAFFIC_BYTES),
-            "traffic_algorithmic": 2 * (S * K + N * K + S * N), "traffic_source": GATE_UP_TRAFFIC_SOURCE,
-            "kernel": "GemmPipeKernel<bf16,256,256> gate/up projection %dx%dx%d" % (S, N, K),
+            "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
+            "traffic": round(GATE_UP_TRAFFIC_BYTES) if GATE_UP_TRAFFIC_BYTES else None,
+            "traffic_algorithmic": 2 * (S * K + N * K + S * N // 2), "traffic_source": GATE_UP_TRAFFIC_SOURCE,
+            "kernel": "GemmPipeKernel<bf16,256,256,8 waves> gate/up projection %dx%dx%d, SwiGLU epilogue"
+                      % (S, N, K),
             "avg_launch_us": round(avg_us, 2), "launches": int(run["gate_up_launches"]),
-            "timing": "HIP events around each launch in an eager pass of the serial prefill"}
+            "timing": "HIP events around each launch in an eager pass of the relay-split prefill",
+            "mfma_util_rocprof": GATE_UP_MFMA_UTIL,
+            "serial_gate_up": {"avg_launch_us": round(ser_us, 2),
+                               "achieved": round(flops / (ser_us * 1e-6) / 1e12, 1),
+                               "note": "the serial program's plain gate/up GEMM (writes the [S, 2I] product)"}}
 
 
 def cpu_baseline(model_dir, seconds_hint=20):
@@ -109,6 +121,24 @@ def profile_gemm(M, N, K, reps):
     print("gemm %dx%dx%d x%d done" % (M, N, K, reps), flush=True)
 
 
+def profile_gemm_swiglu(M, I, K, reps):
+    """One gate/up GEMM launch with SwiGLU in its epilogue per repetition
+    (the relay split's dominant kernel) on random bf16 inputs: the program
+    the rocprofv3 --pmc passes of the roofline's traffic run."""
+    import torch
+
+    from kernrelay_amd import ops
+
+    g = torch.Generator(device="cuda").manual_seed(7)
+    A = torch.randn(M, K, device="cuda", generator=g).to(torch.bfloat16)
+    Bt = (torch.randn(2 * I, K, device="cuda", generator=g) * 0.02).to(torch.bfloat16)
+    act = torch.empty(M, I, device="cuda", dtype=torch.bfloat16)
+    for _ in range(reps):
+        ops.gemm_swiglu_epilogue(A, Bt, act)
+    torch.cuda.synchronize()
+    print("gemm+swiglu %dx%dx%d x%d done" % (M, 2 * I, K, reps), flush=True)
+
+
 def profile_copy(mib, reps):
     """A plain device copy of known size: what FETCH_SIZE / WRITE_SIZE read
     for it calibrates the counters."""
@@ -136,11 +166,16 @@ def main():
     ap.add_argument("--keep", default=None, help="keep / reuse the model directory here")
     ap.add_argument("--profile-gemm", nargs=3, type=int, metavar=("M", "N", "K"),
                     help="only launch the producer GEMM --reps times (for rocprofv3 --pmc)")
+    ap.add_argument("--profile-gemm-swiglu", nargs=3, type=int, metavar=("M", "I", "K"),
+                    help="only launch the gate/up GEMM with SwiGLU epilogue --reps times (for rocprofv3 --pmc)")
     ap.add_argument("--profile-copy", type=int, metavar="MIB", help="only copy MIB MiB --reps times")
     ap.add_argument("--reps", type=int, default=3)
     args = ap.parse_args()
     if args.profile_gemm:
         profile_gemm(*args.profile_gemm, args.reps)
+        return
+    if args.profile_gemm_swiglu:
+        profile_gemm_swiglu(*args.profile_gemm_swiglu, args.reps)
         return
     if args.profile_copy:
         profile_copy(args.profile_copy, args.reps)
@@ -184,7 +219,7 @@ def main():
         if serial["logits_fnv64"] != split["logits_fnv64"]:
             raise RuntimeError("relay split logits differ from serial")
         I, H = cfg["intermediate_size"], cfg["hidden_size"]
-        roof = gemm_roofline(serial, S, 2 * I, H)
+        roof = gemm_roofline(split, serial, S, 2 * I, H)
         total_split_s = sum(split["samples_us"]) / 1e6
         total_serial_s = sum(serial["samples_us"]) / 1e6
         value = args.steps * S / total_split_s

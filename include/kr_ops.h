@@ -112,6 +112,23 @@ int kr_op_gemm_swiglu(int dtype, const void *A, int64_t lda, const void *Bt, int
 int kr_op_gemm_swiglu_epilogue(int dtype, const void *A, int64_t lda, const void *Bt, int64_t ldb, void *act,
                                int64_t ld_act, int M, int cols, int K, void *stream);
 
+/* Stream-K GEMM for shapes whose 256x256 output tiles are fewer than the CUs
+ * (the reference's q/k/v, o and down projections at prefill sizes,
+ * exec/qwen_main.cpp:499-512, 1336-1344): every CU takes an equal run of the
+ * (tile, K stage) iterations, and a tile split between CUs is summed in fixed
+ * piece order by the last of them, so the bits depend on the shape only (a
+ * row-split launch of the same GEMM would differ; use it where no launch is
+ * split). Same operands and rounding as kr_op_gemm (bias added to the
+ * stored product). ws/counters: caller-owned device memory of at least the
+ * sizes kr_op_gemm_streamk_workspace reports; the counters must be zero
+ * before the first launch and are left zero; launches sharing them must be
+ * ordered (one stream). A shape the plan does not cover (0 bytes reported)
+ * runs as kr_op_gemm. */
+int kr_op_gemm_streamk_workspace(int M, int N, int K, size_t *ws_bytes, int *counters);
+int kr_op_gemm_streamk(int dtype, const void *A, int64_t lda, const void *Bt, int64_t ldb, void *C, int64_t ldc,
+                       const void *bias, int M, int N, int K, void *ws, size_t ws_bytes, int32_t *counters,
+                       int n_counters, void *stream);
+
 /* Elementwise op on [rows, cols]; x1 used by mul/add/swiglu; dtype_out
  * differs from dtype_in only for cast. tile_rows = relay granularity
  * (0 = rows); grid = workgroups (0 = sized to the tensor). wait/pub may be

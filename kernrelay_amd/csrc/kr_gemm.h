@@ -35,6 +35,18 @@ struct GemmDesc {
     // rounded as the standalone SwiGLU kernel rounds. C is not written.
     void *epi_act = nullptr;
     int64_t ld_act = 0;
+    // Stream-K (no relay on this launch): when the 256x256 tiles are fewer
+    // than the CUs, every CU takes an equal share of the (tile, K stage)
+    // iterations and split tiles are summed in piece order by their last
+    // piece. Needs the caller's workspace (GemmStreamKNeeds); the counters
+    // must be zero before the first launch and stay owned by one stream.
+    // Bits depend on the shape only, so a launch that never runs row-split
+    // is reproducible; silently data-parallel when the plan does not apply.
+    bool streamk = false;
+    void *sk_ws = nullptr;
+    size_t sk_ws_bytes = 0;
+    int32_t *sk_cnt = nullptr;
+    int sk_cnt_len = 0;
     int order_rows = 0;          // > 0: produce in runs of this many rows (a
                                  // multiple of pub.rows_per_tile), default
                                  // one run per relay tile
@@ -48,6 +60,10 @@ struct GemmDesc {
 // every workgroup first waits for the producer tiles covering its rows of A,
 // and the launch consumes wait.adv_lo..adv_hi once all workgroups are done.
 void GemmLaunch(const GemmDesc &d, hipStream_t stream);
+
+// Workspace a stream-K launch of this shape needs (0 bytes, 0 counters: the
+// launch runs data-parallel).
+void GemmStreamKNeeds(int M, int N, int K, size_t *ws_bytes, int *counters);
 
 struct GemmTile {
     int bm, bn;

@@ -55,6 +55,10 @@ struct GemmParams {
     int tail_cols;
     uint16_t *epi_act;   // SwiGLU epilogue output [M, N/2] (nullptr: store C)
     int64_t ld_act;
+    int sk_wgs;          // stream-K workgroups (0: one tile per workgroup)
+    int sk_pmax;         // partial-sum slots per tile in sk_ws
+    float *sk_ws;        // [tiles][sk_pmax][BM*BN] fp32 partials
+    int32_t *sk_cnt;     // [tiles] arrival counters, zero between launches
     int gemm_wgs;        // workgroups of the GEMM proper; the rest are tail
     int tail_wpt;        // tail workgroups per relay tile
 };
@@ -75,7 +79,7 @@ __device__ __forceinline__ int Swz(int row, int chunk) { return chunk ^ ((row >>
 //   weight, and the blocks the last run read are the ones still cached).
 
 __device__ __forceinline__ void TileOf(int bid, int tiles_m, int tiles_n, int bm, int order_rows, int group_m, int &tm,
-                                       int &tn)
+                                       int &tn, bool xcd = true)
 {
     if (order_rows > 0) {
         const int mt = order_rows / bm;  // row blocks per relay tile
@@ -92,7 +96,7 @@ __device__ __forceinline__ void TileOf(int bid, int tiles_m, int tiles_n, int bm
     // grouped raster: runs of `group_m` row blocks fastest, so an XCD's
     // concurrent tiles form a near-square patch (fewer distinct operand
     // slices per K stage in its L2) rather than a tall column
-    const int t = XcdChunk(bid, 0, tiles_m * tiles_n);
+    const int t = xcd ? XcdChunk(bid, 0, tiles_m * tiles_n) : bid;
     const int gm_all = group_m > 0 ? min(group_m, tiles_m) : tiles_m;
     const int per_group = gm_all * tiles_n;
     const int g = t / per_group;
@@ -519,8 +523,45 @@ int PrefetchStages()
     return v;
 }
 
+// Stream-K plan of a launch: G resident workgroups over tiles x nk
+// iterations, at most pmax pieces per tile.
+struct StreamKPlan {
+    int G = 0, tiles = 0, nk = 0, pmax = 0;
+};
+
+int CuCount()
+{
+    static const int v = [] {
+        int dev = 0, n = 0;
+        if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+            return 256;
+        return n > 0 ? n : 256;
+    }();
+    return v;
+}
+
+// Stream-K for a GEMM whose 256x256 tiles are fewer than the CUs (one
+// workgroup per CU): false when data-parallel tiles already fill the device.
+bool PlanStreamK(int M, int N, int K, StreamKPlan &pl)
+{
+    if (K % kPipeK != 0 || M < 256 || N < 256) return false;
+    pl.G = CuCount();
+    if (const char *e = std::getenv("KR_GEMM_SK_WGS")) pl.G = std::max(1, std::atoi(e));  // measurement aid
+    pl.tiles = ((M + 255) / 256) * ((N + 255) / 256);
+    pl.nk = K / kPipeK;
+    if (pl.tiles >= pl.G || int64_t(pl.tiles) * pl.nk < 4 * int64_t(pl.G)) return false;
+    const int64_t I = int64_t(pl.tiles) * pl.nk;
+    if ((I + pl.G - 1) / pl.G > pl.nk) return false;  // a run spans at most two pieces
+    auto owner = [&](int64_t x) { return int(((x + 1) * pl.G - 1) / I); };
+    pl.pmax = 1;
+    for (int t = 0; t < pl.tiles; ++t)
+        pl.pmax = std::max(pl.pmax, owner(int64_t(t) * pl.nk + pl.nk - 1) - owner(int64_t(t) * pl.nk) + 1);
+    return true;
+}
+
 template <int DT, int BM, int BN>
-void LaunchTyped(const GemmParams &base, int order_rows, int tail_tiles, hipStream_t stream)
+void LaunchTyped(const GemmParams &base, int order_rows, int tail_tiles, hipStream_t stream,
+                 const StreamKPlan *sk = nullptr)
 {
     GemmParams p = base;
     p.tiles_m = (p.M + BM - 1) / BM;
@@ -542,6 +583,12 @@ void LaunchTyped(const GemmParams &base, int order_rows, int tail_tiles, hipStre
     }
     p.gemm_wgs = p.tiles_m * p.tiles_n;
     p.group_m = RasterGroupM();
+    if (sk != nullptr) {
+        if (BM != 256 || BN != 256 || sk->tiles != p.gemm_wgs) throw std::logic_error("gemm: stream-K plan mismatch");
+        p.sk_wgs = sk->G;
+        p.sk_pmax = sk->pmax;
+        p.gemm_wgs = sk->G;
+    }
     int grid_x = p.gemm_wgs;
     if (p.tail_act != nullptr) {
         p.tail_wpt = 256;  // one per CU of the device: enough to fill the idle CUs of the last round
@@ -550,6 +597,11 @@ void LaunchTyped(const GemmParams &base, int order_rows, int tail_tiles, hipStre
     const dim3 grid(grid_x);
     if (p.K % kPipeK == 0 && !ForceSimple()) {
         if constexpr (BM == 256 && BN == 256) {
+            if (sk != nullptr) {
+                hipLaunchKernelGGL((GemmPipeKernel<DT, BM, BN, 0, 8, true>), grid, dim3(512), 0, stream, p);
+                Check(hipGetLastError(), "gemm launch");
+                return;
+            }
             if (PipeWaves() == 8) {
                 hipLaunchKernelGGL((GemmPipeKernel<DT, BM, BN, 0, 8>), grid, dim3(512), 0, stream, p);
                 Check(hipGetLastError(), "gemm launch");
@@ -600,6 +652,18 @@ GemmTile GemmPickTile(int M, int N, int relay_rows, bool coresident)
         }
     }
     return best;
+}
+
+void GemmStreamKNeeds(int M, int N, int K, size_t *ws_bytes, int *counters)
+{
+    StreamKPlan pl;
+    if (PlanStreamK(M, N, K, pl)) {
+        *ws_bytes = size_t(pl.tiles) * pl.pmax * 256 * 256 * 4;
+        *counters = pl.tiles;
+    } else {
+        *ws_bytes = 0;
+        *counters = 0;
+    }
 }
 
 void GemmLaunch(const GemmDesc &d, hipStream_t stream)
@@ -667,6 +731,15 @@ void GemmLaunch(const GemmDesc &d, hipStream_t stream)
     if (d.tail_act != nullptr) {
         const int k = d.M / d.pub.rows_per_tile;
         tail = d.tail_tiles > 0 ? std::min(d.tail_tiles, k) : k;
+    }
+    StreamKPlan skp;
+    if (d.streamk && d.pub.ctrl == nullptr && d.wait.ctrl == nullptr && d.tail_act == nullptr && !ForceSimple() &&
+        d.bm == 0 && d.bn == 0 && PlanStreamK(d.M, d.N, d.K, skp) && d.sk_ws != nullptr && d.sk_cnt != nullptr &&
+        d.sk_ws_bytes >= size_t(skp.tiles) * skp.pmax * 256 * 256 * 4 && d.sk_cnt_len >= skp.tiles) {
+        p.sk_ws = static_cast<float *>(d.sk_ws);
+        p.sk_cnt = d.sk_cnt;
+        bf ? LaunchTyped<kBF16, 256, 256>(p, 0, 0, stream, &skp) : LaunchTyped<kF16, 256, 256>(p, 0, 0, stream, &skp);
+        return;
     }
 #define KR_GEMM_CASE(BM_, BN_)                                                                     \
     if (t.bm == BM_ && t.bn == BN_) {                                                              \

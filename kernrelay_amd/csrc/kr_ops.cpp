@@ -116,6 +116,40 @@ int kr_op_gemm_swiglu(int dtype, const void *A, int64_t lda, const void *Bt, int
     });
 }
 
+int kr_op_gemm_streamk_workspace(int M, int N, int K, size_t *ws_bytes, int *counters)
+{
+    return Guard([&] {
+        if (ws_bytes == nullptr || counters == nullptr) throw std::runtime_error("null output pointer");
+        kr::GemmStreamKNeeds(M, N, K, ws_bytes, counters);
+    });
+}
+
+int kr_op_gemm_streamk(int dtype, const void *A, int64_t lda, const void *Bt, int64_t ldb, void *C, int64_t ldc,
+                       const void *bias, int M, int N, int K, void *ws, size_t ws_bytes, int32_t *counters,
+                       int n_counters, void *stream)
+{
+    return Guard([&] {
+        kr::GemmDesc d;
+        d.dtype = dtype;
+        d.A = A;
+        d.Bt = Bt;
+        d.C = C;
+        d.bias = bias;
+        d.lda = lda;
+        d.ldb = ldb;
+        d.ldc = ldc;
+        d.M = M;
+        d.N = N;
+        d.K = K;
+        d.streamk = true;
+        d.sk_ws = ws;
+        d.sk_ws_bytes = ws_bytes;
+        d.sk_cnt = counters;
+        d.sk_cnt_len = n_counters;
+        kr::GemmLaunch(d, S(stream));
+    });
+}
+
 int kr_op_gemm_swiglu_epilogue(int dtype, const void *A, int64_t lda, const void *Bt, int64_t ldb, void *act,
                                int64_t ld_act, int M, int cols, int K, void *stream)
 {

@@ -52,11 +52,16 @@ def _lib():
         L.kr_op_gemm_swiglu.argtypes = [i32, vp, i64, vp, i64, vp, vp, i32, i32, i32, ctypes.POINTER(KrPub),
                                         i32, i32, vp]
         L.kr_op_gemm_swiglu_epilogue.argtypes = [i32, vp, i64, vp, i64, vp, i64, i32, i32, i32, vp]
+        L.kr_op_gemm_streamk_workspace.argtypes = [i32, i32, i32, ctypes.POINTER(ctypes.c_size_t),
+                                                    ctypes.POINTER(ctypes.c_int)]
+        L.kr_op_gemm_streamk.argtypes = [i32, vp, i64, vp, i64, vp, i64, vp, i32, i32, i32, vp, ctypes.c_size_t, vp,
+                                         i32, vp]
         L.kr_op_stream_create.argtypes = []
         L.kr_op_stream_create.restype = vp
         L.kr_op_stream_destroy.argtypes = [vp]
         L.kr_op_stream_destroy.restype = ctypes.c_int
-        for name in ("kr_op_gemm", "kr_op_gemm_swiglu", "kr_op_gemm_swiglu_epilogue", "kr_op_elementwise", "kr_op_rowop", "kr_op_wait", "kr_op_publish",
+        for name in ("kr_op_gemm", "kr_op_gemm_swiglu", "kr_op_gemm_swiglu_epilogue", "kr_op_gemm_streamk",
+                     "kr_op_gemm_streamk_workspace", "kr_op_elementwise", "kr_op_rowop", "kr_op_wait", "kr_op_publish",
                      "kr_op_embedding", "kr_op_rope", "kr_op_attention", "kr_op_transpose"):
             getattr(L, name).restype = ctypes.c_int
         _BOUND = True
@@ -139,6 +144,24 @@ def gemm_swiglu(A, Bt, C, act, pub, tail_tiles=0, order_rows=0, stream=None):
     assert Bt.shape == (2 * cols, K) and C.shape == (M, 2 * cols) and act.shape[0] == M
     _check(_lib().kr_op_gemm_swiglu(_dt(A), _ptr(A), A.stride(0), _ptr(Bt), Bt.stride(0), _ptr(C), _ptr(act),
                                     M, cols, K, ctypes.byref(pub), tail_tiles, order_rows, _stream(stream)))
+
+
+def gemm_streamk_workspace(M, N, K):
+    """(workspace bytes, counters) a stream-K GEMM of this shape needs; (0, 0)
+    when it runs data-parallel."""
+    b, c = ctypes.c_size_t(0), ctypes.c_int(0)
+    _check(_lib().kr_op_gemm_streamk_workspace(M, N, K, ctypes.byref(b), ctypes.byref(c)))
+    return b.value, c.value
+
+
+def gemm_streamk(A, Bt, C, ws, counters, bias=None, stream=None):
+    """C = A @ Bt^T (+bias) split stream-K over the CUs (ws: uint8 device
+    tensor, counters: int32 device tensor, zero before the first call)."""
+    M, K = A.shape
+    N = Bt.shape[0]
+    _check(_lib().kr_op_gemm_streamk(_dt(A), _ptr(A), A.stride(0), _ptr(Bt), Bt.stride(0), _ptr(C), C.stride(0),
+                                     _ptr(bias), M, N, K, _ptr(ws), ws.numel() * ws.element_size(),
+                                     _ptr(counters), counters.numel(), _stream(stream)))
 
 
 def gemm_swiglu_epilogue(A, Bt, act, stream=None):

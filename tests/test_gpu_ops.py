@@ -404,3 +404,35 @@ def test_gemm_swiglu_epilogue_bit_exact(gpu, M, I, K):
     close(ref_c, O.gemm(A.cpu(), Bt.cpu().t()))
     g = ref_c.cpu().view(M, I // 8, 2, 8)
     close(act, O.swiglu(g[:, :, 0, :].reshape(M, I), g[:, :, 1, :].reshape(M, I)))
+
+
+@pytest.mark.parametrize("M,N,K,bias", [(2048, 4608, 3584, True), (2048, 3584, 3584, False),
+                                        (2048, 3584, 18944, False), (1000, 2560, 4096, True)])
+def test_gemm_streamk(gpu, M, N, K, bias):
+    """Stream-K over the CUs (the under-filled q/k/v, o and down shapes, and a
+    ragged one): matches the oracle and the data-parallel kernel within the
+    bf16 bar, repeats bit for bit (fixed piece order), leaves its counters
+    zero and writes nothing outside C."""
+    announce("gemm stream-K %dx%dx%d bias=%s" % (M, N, K, bias))
+    nbytes, ncnt = ops.gemm_streamk_workspace(M, N, K)
+    assert nbytes > 0 and ncnt > 0
+    A = rand((M, K), 1.0, 50).cuda()
+    Bt = rand((N, K), 0.02, 51).cuda()
+    b = rand((N,), 0.5, 52).cuda() if bias else None
+    ws = torch.empty(nbytes, dtype=torch.uint8, device="cuda")
+    cnt = torch.zeros(ncnt, dtype=torch.int32, device="cuda")
+    pad = torch.full((M + 4, N + 8), 3.0, dtype=torch.bfloat16, device="cuda")
+    C = pad[:M, :N]
+    ops.gemm_streamk(A, Bt, C, ws, cnt, bias=b)
+    first = C.clone()
+    for _ in range(2):
+        C.zero_()
+        ops.gemm_streamk(A, Bt, C, ws, cnt, bias=b)
+        torch.cuda.synchronize()
+        assert torch.equal(C, first)
+    assert int(cnt.abs().sum()) == 0
+    assert torch.all(pad[M:] == 3.0) and torch.all(pad[:, N:] == 3.0)
+    dp = torch.empty(M, N, dtype=torch.bfloat16, device="cuda")
+    ops.gemm(A, Bt, dp, bias=b)
+    close(C, dp)
+    close(C, O.gemm(A.cpu(), Bt.cpu().t(), bias=b.cpu() if bias else None))
