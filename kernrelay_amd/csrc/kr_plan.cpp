@@ -651,9 +651,9 @@ private:
     // How many leading tiles of consumer launch L its producer launch PL
     // releases before its last round of workgroups starts: a persistent
     // consumer beside the GEMM can only overlap those; the rest are released
-    // when the GEMM ends and run better at full width. -1 when PL is not one
-    // GEMM launch releasing every tile of its node (then every tile waits
-    // in-kernel).
+    // when the GEMM ends and run better at full width. -1 (every tile waits
+    // in-kernel) when PL is not one GEMM launch releasing every tile of its
+    // node, or when the tail is small enough for the persistent grid.
     int EarlyTiles(const Launch &PL, const Launch &L, int64_t in_off, int64_t in_rows) const
     {
         const NodeSpec &P = *PL.node;
@@ -672,6 +672,9 @@ private:
         const int nt = int((in_rows + prows - 1) / prows);
         int early = 0;
         while (early < nt && (int64_t(k0 + early) + 1) * per <= last_round) ++early;
+        // a tail the persistent grid clears in one pass (a wave per row,
+        // four rows per workgroup) gains nothing from a second launch
+        if (in_rows - int64_t(early) * prows <= int64_t(relay_grid_) * 4) return -1;
         return early;
     }
 
