@@ -463,6 +463,36 @@ GemmKernel(GemmParams p)
     RelayFinish(p.wait);
 }
 
+// Stream-K partial sums move as 16-byte device-scope accesses (written
+// through to memory / read past this XCD's L2, which may hold stale lines of
+// the workspace from an earlier launch).
+__device__ __forceinline__ void PutF32x4Dev(float *p, float a, float b, float c, float d)
+{
+    const RelayU32x4 w = {__float_as_uint(a), __float_as_uint(b), __float_as_uint(c), __float_as_uint(d)};
+    // two wait states before the data VGPRs may be rewritten (as PutU128)
+    asm volatile("global_store_dwordx4 %0, %1, off sc1\n\ts_nop 1" ::"v"(p), "v"(w) : "memory");
+}
+
+// Eight 16-byte device-scope loads p + u * stride (floats), in flight
+// together; returns once all have landed.
+__device__ __forceinline__ void GetF32x4x8Dev(const float *p, int64_t stride, RelayU32x4 (&r)[8])
+{
+    asm volatile(
+        "global_load_dwordx4 %0, %8, off sc1\n\t"
+        "global_load_dwordx4 %1, %9, off sc1\n\t"
+        "global_load_dwordx4 %2, %10, off sc1\n\t"
+        "global_load_dwordx4 %3, %11, off sc1\n\t"
+        "global_load_dwordx4 %4, %12, off sc1\n\t"
+        "global_load_dwordx4 %5, %13, off sc1\n\t"
+        "global_load_dwordx4 %6, %14, off sc1\n\t"
+        "global_load_dwordx4 %7, %15, off sc1\n\t"
+        "s_waitcnt vmcnt(0)"
+        : "=&v"(r[0]), "=&v"(r[1]), "=&v"(r[2]), "=&v"(r[3]), "=&v"(r[4]), "=&v"(r[5]), "=&v"(r[6]), "=&v"(r[7])
+        : "v"(p), "v"(p + stride), "v"(p + 2 * stride), "v"(p + 3 * stride), "v"(p + 4 * stride),
+          "v"(p + 5 * stride), "v"(p + 6 * stride), "v"(p + 7 * stride)
+        : "memory");
+}
+
 // ---------------------------------------------------------------------------
 #include "kr_gemm_pipe.inc"
 
