@@ -542,6 +542,26 @@ int PipeWaves()
     return v;
 }
 
+// Main loop of the 8-wave 256x256 kernel (KR_GEMM_LOOP): 2 (default) =
+// register-staged refills spread evenly over each stage, 0 = two 64-deep
+// direct-to-LDS stages refilled in a burst after each stage's barrier,
+// 1 = ping-pong (the two waves of a SIMD alternate memory and MFMA phases),
+// 4 / 5 = a ring of four / five 32-deep direct-to-LDS stages. Timing only,
+// never the bits. Measured on MI355X (us): 4096^3 0: 126.7, 1: 140.1,
+// 2: 118.5, 4: 142.7, 5: 141.3; gate/up 2048x37888x3584 561 / 583 / 529 /
+// 630 / 616; QKV 2048x4608x3584 103 / 114 / 85 / 111 / 113. (The 4-wave
+// 256x128 and 128x256 kernels keep their three-stage direct-to-LDS ring,
+// which already spreads its refills: staged, they measured 4-8% slower.)
+int MainLoopMode()
+{
+    static const int v = [] {
+        const char *e = std::getenv("KR_GEMM_LOOP");
+        const int m = e != nullptr ? std::atoi(e) : 2;
+        return m == 0 || m == 1 || m == 4 || m == 5 ? m : 2;
+    }();
+    return v;
+}
+
 // L2 prefetch distance of the pipelined kernel in K stages (KR_GEMM_PF: 0
 // default = off, 2, 4); it changes timing only, never the bits.
 int PrefetchStages()
@@ -628,12 +648,19 @@ void LaunchTyped(const GemmParams &base, int order_rows, int tail_tiles, hipStre
     if (p.K % kPipeK == 0 && !ForceSimple()) {
         if constexpr (BM == 256 && BN == 256) {
             if (sk != nullptr) {
-                hipLaunchKernelGGL((GemmPipeKernel<DT, BM, BN, 0, 8, true>), grid, dim3(512), 0, stream, p);
+                if (MainLoopMode() == 2) hipLaunchKernelGGL((GemmPipeKernel<DT, BM, BN, 0, 8, true, 2>), grid, dim3(512), 0, stream, p);
+                else hipLaunchKernelGGL((GemmPipeKernel<DT, BM, BN, 0, 8, true>), grid, dim3(512), 0, stream, p);
                 Check(hipGetLastError(), "gemm launch");
                 return;
             }
             if (PipeWaves() == 8) {
-                hipLaunchKernelGGL((GemmPipeKernel<DT, BM, BN, 0, 8>), grid, dim3(512), 0, stream, p);
+                switch (MainLoopMode()) {
+                case 1: hipLaunchKernelGGL((GemmPipeKernel<DT, BM, BN, 0, 8, false, 1>), grid, dim3(512), 0, stream, p); break;
+                case 2: hipLaunchKernelGGL((GemmPipeKernel<DT, BM, BN, 0, 8, false, 2>), grid, dim3(512), 0, stream, p); break;
+                case 4: hipLaunchKernelGGL((GemmPipeKernel<DT, BM, BN, 0, 8, false, 4>), grid, dim3(512), 0, stream, p); break;
+                case 5: hipLaunchKernelGGL((GemmPipeKernel<DT, BM, BN, 0, 8, false, 5>), grid, dim3(512), 0, stream, p); break;
+                default: hipLaunchKernelGGL((GemmPipeKernel<DT, BM, BN, 0, 8>), grid, dim3(512), 0, stream, p); break;
+                }
                 Check(hipGetLastError(), "gemm launch");
                 return;
             }
@@ -660,8 +687,8 @@ int Waves(int tiles, int slots) { return (tiles + slots - 1) / slots; }
 GemmTile GemmPickTile(int M, int N, int relay_rows, bool coresident)
 {
     // Candidates from most to least data reuse; take the first that keeps the
-    // device busy (>= 2 full waves of workgroups) or, failing that, the one
-    // with the best wave efficiency. Every tile runs the same MFMA and K order,
+    // device busy (>= 2 full waves of workgroups, or whole waves) or, failing
+    // that, the one with the best wave efficiency. Every tile runs the same MFMA and K order,
     // so the choice never changes the arithmetic.
     static const GemmTile cands[] = {{256, 256}, {256, 128}, {128, 256}, {128, 128}, {64, 256}};
     const int cus = 256;
@@ -672,7 +699,8 @@ GemmTile GemmPickTile(int M, int N, int relay_rows, bool coresident)
         if (coresident && t.bm * t.bn >= 256 * 256) continue;
         const int tiles = ((M + t.bm - 1) / t.bm) * ((N + t.bn - 1) / t.bn);
         const int slots = cus * (t.bm * t.bn >= 256 * 128 ? 1 : 2);
-        if (tiles >= 2 * slots) return t;
+        // enough workgroups for two rounds, or whole rounds exactly
+        if (tiles >= 2 * slots || tiles % slots == 0) return t;
         const double work = double(t.bm) * t.bn;  // per-workgroup work unit
         const double eff = double(tiles) * work / (double(Waves(tiles, slots)) * slots * work);
         const double score = eff * (t.bm * t.bn >= 256 * 128 ? 1.0 : 0.85);
