@@ -544,20 +544,20 @@ int PipeWaves()
 
 // Main loop of the 8-wave 256x256 kernel (KR_GEMM_LOOP): 2 (default) =
 // register-staged refills spread evenly over each stage, 0 = two 64-deep
-// direct-to-LDS stages refilled in a burst after each stage's barrier,
-// 1 = ping-pong (the two waves of a SIMD alternate memory and MFMA phases),
-// 4 / 5 = a ring of four / five 32-deep direct-to-LDS stages. Timing only,
-// never the bits. Measured on MI355X (us): 4096^3 0: 126.7, 1: 140.1,
-// 2: 118.5, 4: 142.7, 5: 141.3; gate/up 2048x37888x3584 561 / 583 / 529 /
-// 630 / 616; QKV 2048x4608x3584 103 / 114 / 85 / 111 / 113. (The 4-wave
-// 256x128 and 128x256 kernels keep their three-stage direct-to-LDS ring,
-// which already spreads its refills: staged, they measured 4-8% slower.)
+// direct-to-LDS stages refilled in a burst after each stage's barrier.
+// Timing only, never the bits. Measured on MI355X (us, 0 / 2): 4096^3
+// 126.7 / 118.5, gate/up 2048x37888x3584 561 / 529, QKV 2048x4608x3584
+// 103 / 85, lm_head 2048x152064x3584 1967 / 1871. Two other schedules
+// measured slower than both: the two waves of a SIMD alternating memory and
+// MFMA phases (4096^3 140 us), and a ring of four or five 32-deep
+// direct-to-LDS stages (142 us: half-line requests). The 4-wave 256x128 and
+// 128x256 kernels keep their three-stage direct-to-LDS ring, which already
+// spreads its refills: staged, they measured 4-8% slower.
 int MainLoopMode()
 {
     static const int v = [] {
         const char *e = std::getenv("KR_GEMM_LOOP");
-        const int m = e != nullptr ? std::atoi(e) : 2;
-        return m == 0 || m == 1 || m == 4 || m == 5 ? m : 2;
+        return e != nullptr && std::atoi(e) == 0 ? 0 : 2;
     }();
     return v;
 }
@@ -590,16 +590,29 @@ int CuCount()
     return v;
 }
 
-// Stream-K for a GEMM whose 256x256 tiles are fewer than the CUs (one
-// workgroup per CU): false when data-parallel tiles already fill the device.
+// Stream-K plan of a GEMM whose 256x256 tiles leave CUs idle. Default: an
+// exact split of K, S = CUs / tiles pieces per tile (S >= 2), capped so that
+// every piece keeps at least 64 K stages (shorter pieces do not repay the
+// fp32 partials and the fix-up), so every workgroup runs one piece and the
+// workgroups of an XCD walk K in step on a compact patch of tiles. Measured
+// on MI355X: down 2048x3584x18944 258 us (S = 2) against 288 us for the best
+// data-parallel tiles; spreading the iterations over all 256 CUs instead
+// (pieces of uneven length, two or three per tile at different K offsets,
+// sharing no operand lines) took 369 us. KR_GEMM_SK_WGS=G forces that even
+// spread over G workgroups (a measurement aid).
 bool PlanStreamK(int M, int N, int K, StreamKPlan &pl)
 {
     if (K % kPipeK != 0 || M < 256 || N < 256) return false;
-    pl.G = CuCount();
-    if (const char *e = std::getenv("KR_GEMM_SK_WGS")) pl.G = std::max(1, std::atoi(e));  // measurement aid
     pl.tiles = ((M + 255) / 256) * ((N + 255) / 256);
     pl.nk = K / kPipeK;
-    if (pl.tiles >= pl.G || int64_t(pl.tiles) * pl.nk < 4 * int64_t(pl.G)) return false;
+    if (const char *e = std::getenv("KR_GEMM_SK_WGS")) {
+        pl.G = std::max(1, std::atoi(e));
+        if (pl.tiles >= pl.G || int64_t(pl.tiles) * pl.nk < 4 * int64_t(pl.G)) return false;
+    } else {
+        const int S = std::min(CuCount() / pl.tiles, pl.nk / 64);
+        if (S < 2) return false;
+        pl.G = S * pl.tiles;
+    }
     const int64_t I = int64_t(pl.tiles) * pl.nk;
     if ((I + pl.G - 1) / pl.G > pl.nk) return false;  // a run spans at most two pieces
     auto owner = [&](int64_t x) { return int(((x + 1) * pl.G - 1) / I); };
@@ -619,7 +632,15 @@ void LaunchTyped(const GemmParams &base, int order_rows, int tail_tiles, hipStre
     // relay order needs whole relay tiles of whole row blocks
     auto whole = [&](int rows) { return rows > 0 && rows % BM == 0 && p.tiles_m % (rows / BM) == 0; };
     p.order_rows = 0;
-    if (p.pub.ctrl != nullptr) {
+    if (p.pub.ctrl != nullptr && sk != nullptr) {
+        // stream-K: each tile's finisher arrives once on every relay tile its
+        // rows cover, so a relay tile waits for (row blocks in it) x tiles_n
+        // arrivals, or tiles_n when it is shorter than a row block
+        const int R = p.pub.rows_per_tile;
+        if (R <= 0 || (R % BM != 0 && BM % R != 0) || p.M % R != 0)
+            throw std::runtime_error("gemm: stream-K relay tiles must be whole row blocks or divide one");
+        p.pub.arrivals = (R >= BM ? R / BM : 1) * p.tiles_n;
+    } else if (p.pub.ctrl != nullptr) {
         if (!whole(p.pub.rows_per_tile)) throw std::runtime_error("relay tile rows must be a multiple of BM dividing M");
         p.pub.arrivals = (p.pub.rows_per_tile / BM) * p.tiles_n;
         p.order_rows = p.pub.rows_per_tile;
@@ -654,13 +675,8 @@ void LaunchTyped(const GemmParams &base, int order_rows, int tail_tiles, hipStre
                 return;
             }
             if (PipeWaves() == 8) {
-                switch (MainLoopMode()) {
-                case 1: hipLaunchKernelGGL((GemmPipeKernel<DT, BM, BN, 0, 8, false, 1>), grid, dim3(512), 0, stream, p); break;
-                case 2: hipLaunchKernelGGL((GemmPipeKernel<DT, BM, BN, 0, 8, false, 2>), grid, dim3(512), 0, stream, p); break;
-                case 4: hipLaunchKernelGGL((GemmPipeKernel<DT, BM, BN, 0, 8, false, 4>), grid, dim3(512), 0, stream, p); break;
-                case 5: hipLaunchKernelGGL((GemmPipeKernel<DT, BM, BN, 0, 8, false, 5>), grid, dim3(512), 0, stream, p); break;
-                default: hipLaunchKernelGGL((GemmPipeKernel<DT, BM, BN, 0, 8>), grid, dim3(512), 0, stream, p); break;
-                }
+                if (MainLoopMode() == 2) hipLaunchKernelGGL((GemmPipeKernel<DT, BM, BN, 0, 8, false, 2>), grid, dim3(512), 0, stream, p);
+                else hipLaunchKernelGGL((GemmPipeKernel<DT, BM, BN, 0, 8>), grid, dim3(512), 0, stream, p);
                 Check(hipGetLastError(), "gemm launch");
                 return;
             }
@@ -791,7 +807,12 @@ void GemmLaunch(const GemmDesc &d, hipStream_t stream)
         tail = d.tail_tiles > 0 ? std::min(d.tail_tiles, k) : k;
     }
     StreamKPlan skp;
-    if (d.streamk && d.pub.ctrl == nullptr && d.wait.ctrl == nullptr && d.tail_act == nullptr && !ForceSimple() &&
+    // (a publishing split needs relay tiles that are whole 256-row blocks or
+    // divide one)
+    const int rpt = d.pub.rows_per_tile;
+    const bool sk_pub_ok =
+        d.pub.ctrl == nullptr || (rpt > 0 && (rpt % 256 == 0 || 256 % rpt == 0) && d.M % rpt == 0);
+    if (d.streamk && sk_pub_ok && d.wait.ctrl == nullptr && d.tail_act == nullptr && d.epi_act == nullptr && !ForceSimple() &&
         d.bm == 0 && d.bn == 0 && PlanStreamK(d.M, d.N, d.K, skp) && d.sk_ws != nullptr && d.sk_cnt != nullptr &&
         d.sk_ws_bytes >= size_t(skp.tiles) * skp.pmax * 256 * 256 * 4 && d.sk_cnt_len >= skp.tiles) {
         p.sk_ws = static_cast<float *>(d.sk_ws);

@@ -521,6 +521,43 @@ private:
         a16(xf_, S * H_);
         a16(logits_, S * size_t(V_));
         rstd_.Alloc(S * 4);
+        // KR_QWEN_SPLITK=1: plain GEMMs split K over idle CUs where the
+        // GEMM planner finds an exact split (at seq 2048 the down projection,
+        // 2 pieces per tile). Off by default: in the prefill the down GEMM's
+        // input was just written and sits in the MALL, and data-parallel
+        // 256x128 tiles measured 245 us per launch against 257 us split
+        // (cold operands: 288 against 258). One workspace serves every plain
+        // GEMM (they run one after another on the producer stream), sized for
+        // whole-sequence and row-slice shapes; its tile counters start at
+        // zero and every split GEMM leaves them at zero.
+        for (int k = 1; k <= 8 && EnvInt("KR_QWEN_SPLITK", 0) != 0; k *= 2) {
+            const int M = seq_ / k;
+            const int shapes[][2] = {{int(ldqkv_), H_}, {H_, HQ_ * D_}, {2 * I_, H_}, {I_, H_}, {H_, I_}, {int(V_), H_}};
+            for (const auto &nk : shapes) {
+                size_t b = 0;
+                int c = 0;
+                GemmStreamKNeeds(M, nk[0], nk[1], &b, &c);
+                skws_bytes_ = std::max(skws_bytes_, b);
+                skcnt_len_ = std::max(skcnt_len_, c);
+            }
+        }
+        if (skws_bytes_ > 0) {
+            skws_.Alloc(skws_bytes_);
+            skcnt_.Alloc(size_t(skcnt_len_) * 4);
+            Check(hipMemset(skcnt_.get(), 0, skcnt_.bytes()), "zero stream-K counters");
+        }
+    }
+
+    // Plain GEMMs may split K over idle CUs (GemmLaunch decides per shape;
+    // no workspace without KR_QWEN_SPLITK).
+    void WithStreamK(GemmDesc &d) const
+    {
+        if (skws_bytes_ == 0) return;
+        d.streamk = true;
+        d.sk_ws = skws_.get();
+        d.sk_ws_bytes = skws_bytes_;
+        d.sk_cnt = skcnt_.as<int32_t>();
+        d.sk_cnt_len = skcnt_len_;
     }
 
     // ------------------------------------------------------------ program
@@ -610,6 +647,7 @@ private:
         d.K = K;
         d.pub = pub;
         d.wait = wait;
+        WithStreamK(d);
         Emit(s, [d](hipStream_t st) { GemmLaunch(d, st); });
     }
 
@@ -970,6 +1008,9 @@ private:
     std::vector<Item> prog_;
     std::vector<std::pair<hipGraph_t, hipGraphExec_t>> graphs_;
     DevBuf ctrl_;
+    DevBuf skws_, skcnt_;  // stream-K partials and tile counters
+    size_t skws_bytes_ = 0;
+    int skcnt_len_ = 0;
     size_t ctrl_blocks_ = 0;
     std::vector<int> consumed_;
     std::map<int, hipEvent_t> edge_event_;
@@ -1050,6 +1091,7 @@ std::string Model::ProfileMany(const std::string &spec_path)
                     d.M = per;
                     d.N = int(N);
                     d.K = int(K);
+                    WithStreamK(d);
                     calls.push_back([d](hipStream_t s) { GemmLaunch(d, s); });
                 }
             } else if (op == "add" || op == "mul" || op == "silu" || op == "swiglu") {

@@ -5,6 +5,8 @@ Tolerance for bf16 outputs: |gpu - oracle| <= 2e-2 + 1e-2 * |oracle|
 bit-exact; the relay split bit-exact against the unsplit kernel.
 """
 
+import os
+
 import numpy as np
 import pytest
 import torch
@@ -406,14 +408,35 @@ def test_gemm_swiglu_epilogue_bit_exact(gpu, M, I, K):
     close(act, O.swiglu(g[:, :, 0, :].reshape(M, I), g[:, :, 1, :].reshape(M, I)))
 
 
-@pytest.mark.parametrize("M,N,K,bias", [(2048, 4608, 3584, True), (2048, 3584, 3584, False),
-                                        (2048, 3584, 18944, False), (1000, 2560, 4096, True)])
-def test_gemm_streamk(gpu, M, N, K, bias):
-    """Stream-K over the CUs (the under-filled q/k/v, o and down shapes, and a
-    ragged one): matches the oracle and the data-parallel kernel within the
-    bf16 bar, repeats bit for bit (fixed piece order), leaves its counters
-    zero and writes nothing outside C."""
-    announce("gemm stream-K %dx%dx%d bias=%s" % (M, N, K, bias))
+@pytest.mark.parametrize("M,N,K,bias,wgs", [(2048, 3584, 18944, False, None), (1000, 2560, 16384, True, None),
+                                            (2048, 4608, 3584, True, 256), (2048, 3584, 3584, False, 256)])
+def test_gemm_streamk(gpu, M, N, K, bias, wgs):
+    """Stream-K: the default exact split of K (the down shape: two pieces per
+    tile; a ragged one: four) and, forced over 256 workgroups, the uneven
+    spread (the q/k/v and o shapes: pieces of unequal length, up to three per
+    tile): matches the oracle and the data-parallel kernel within the bf16
+    bar, repeats bit for bit (fixed piece order), leaves its counters zero
+    and writes nothing outside C."""
+    announce("gemm stream-K %dx%dx%d bias=%s wgs=%s" % (M, N, K, bias, wgs))
+    if wgs is not None:
+        os.environ["KR_GEMM_SK_WGS"] = str(wgs)
+    try:
+        _streamk_case(M, N, K, bias)
+    finally:
+        os.environ.pop("KR_GEMM_SK_WGS", None)
+
+
+def test_gemm_streamk_policy(gpu):
+    """The default plan splits K only where whole pieces of >= 64 K stages
+    fill idle CUs: the down shape (112 tiles, 296 stages) splits in two, the
+    o and q/k/v shapes (56 stages) and a full-device shape do not."""
+    assert ops.gemm_streamk_workspace(2048, 3584, 18944) == (112 * 2 * 256 * 256 * 4, 112)
+    assert ops.gemm_streamk_workspace(2048, 3584, 3584) == (0, 0)
+    assert ops.gemm_streamk_workspace(2048, 4608, 3584) == (0, 0)
+    assert ops.gemm_streamk_workspace(4096, 4096, 18944) == (0, 0)
+
+
+def _streamk_case(M, N, K, bias):
     nbytes, ncnt = ops.gemm_streamk_workspace(M, N, K)
     assert nbytes > 0 and ncnt > 0
     A = rand((M, K), 1.0, 50).cuda()

@@ -63,6 +63,36 @@ def test_all_modes_bit_exact_and_match_oracle(gpu, tmp_path, preset):
         assert r["logits_fnv64"] == fnv, (mode, r["logits_fnv64"], fnv)
 
 
+def test_split_k_down_all_modes_bit_exact(gpu, tmp_path):
+    """With KR_QWEN_SPLITK, layer shapes whose down projection splits K over
+    idle CUs (I 8192 at seq 512: 4 output tiles of 128 K stages, two pieces
+    each): every mode runs
+    the same split (relay_flag releases its relay tile from the split's
+    finishers), so the logits stay bit-identical across modes and match the
+    oracle."""
+    from kernrelay_amd import ops
+    cfg = dict(modeldir.PRESETS["tiny-qwen3"])
+    cfg["intermediate_size"] = 8192
+    seq = 512
+    assert ops.gemm_streamk_workspace(seq, cfg["hidden_size"], 8192)[0] > 0  # the down GEMM splits
+    d = modeldir.write_model_dir(tmp_path / "splitk", cfg, seq=seq)
+    ref = oq.write_reference(d)
+    fnv = None
+    os.environ["KR_QWEN_SPLITK"] = "1"
+    try:
+        for mode in MODES:
+            dump = tmp_path / ("dump_" + mode.replace(":", "_"))
+            dump.mkdir()
+            r = run(d, mode, seq, dump)
+            assert r["flag_timeouts"] == 0, (mode, r)
+            check_logits(dump, ref)
+            if fnv is None:
+                fnv = r["logits_fnv64"]
+            assert r["logits_fnv64"] == fnv, (mode, r["logits_fnv64"], fnv)
+    finally:
+        del os.environ["KR_QWEN_SPLITK"]
+
+
 def test_qwen05_shapes_split_bit_exact(gpu, tmp_path):
     """Qwen2.5-0.5B layer shapes (H 896, 14/2 heads, D 64, I 4864, V 151936,
     tied) at seq 2048, two layers: serial == relay_split:4 (SwiGLU in the
