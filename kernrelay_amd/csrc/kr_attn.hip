@@ -20,7 +20,8 @@
 // {4h..4h+3, 8+4h..8+4h+3} for lane half h; V^T rows are stored with the keys
 // of each 16-key group permuted into exactly that order, so one ds_read_b128
 // fetches a lane's 8 keys.
-// Online softmax in base 2 (scores pre-scaled by scale*log2(e)), fp32 state.
+// Online softmax in base 2 (exponent fma(score, scale*log2(e), -m)), fp32
+// state, with the running max m moved lazily (see the loop).
 // Workgroups run heaviest (longest causal rows) first across all heads.
 #include "kr_misc.h"
 
@@ -195,39 +196,49 @@ __global__ void __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_wav
                 }
             }
 
+            // raw scores: the row max is taken before scaling (scale > 0);
+            // masked keys (above the diagonal, past S) by select, not branch
             float mloc = -INFINITY;
             const bool diag = kv0 + kKvBlk - 1 > q0 + wave * 32 || kv0 + kKvBlk > p.S;
+            if (diag) {
+#pragma unroll
+                for (int kh = 0; kh < 2; ++kh)
+#pragma unroll
+                    for (int v = 0; v < 16; ++v) {
+                        const int kv = kv0 + kh * 32 + 8 * (v >> 2) + 4 * hf + (v & 3);
+                        sacc[kh][v] = kv > qrow || kv >= p.S ? -INFINITY : sacc[kh][v];
+                    }
+            }
 #pragma unroll
             for (int kh = 0; kh < 2; ++kh)
 #pragma unroll
-                for (int v = 0; v < 16; ++v) {
-                    float s = sacc[kh][v] * p.scale_log2;
-                    if (diag) {
-                        const int kv = kv0 + kh * 32 + 8 * (v >> 2) + 4 * hf + (v & 3);
-                        if (kv > qrow || kv >= p.S) s = -INFINITY;
-                    }
-                    sacc[kh][v] = s;
-                    mloc = fmaxf(mloc, s);
-                }
-            mloc = fmaxf(mloc, __shfl_xor(mloc, 32, 64));
-            const float mnew = fmaxf(m, mloc);
+                for (int v = 0; v < 16; ++v) mloc = fmaxf(mloc, sacc[kh][v]);
+            mloc = fmaxf(mloc, __shfl_xor(mloc, 32, 64)) * p.scale_log2;
+            // lazy rescale: the row's reference max m moves only when a score
+            // exceeds it by more than 2^8 (so p = 2^(s - m) <= 256, exact in
+            // range for bf16 P and fp32 sums); the wave skips the O rescale
+            // when no row moved. O / l is unchanged: both carry the same m.
+            const bool move = mloc > m + 8.0f;
+            const float mnew = move ? mloc : m;
             const float msub = mnew == -INFINITY ? 0.0f : mnew;
-            const float alpha = __builtin_amdgcn_exp2f(m - msub);
+            const float alpha = move ? __builtin_amdgcn_exp2f(m - msub) : 1.0f;
             float lsum = 0.0f;
 #pragma unroll
             for (int kh = 0; kh < 2; ++kh)
 #pragma unroll
                 for (int v = 0; v < 16; ++v) {
-                    const float pv = __builtin_amdgcn_exp2f(sacc[kh][v] - msub);
+                    const float pv = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[kh][v], p.scale_log2, -msub));
                     sacc[kh][v] = pv;
                     lsum += pv;
                 }
             l = l * alpha + lsum;
             m = mnew;
+            if (__builtin_amdgcn_read_exec() & __ballot(move)) {
 #pragma unroll
-            for (int b = 0; b < DBLK; ++b)
+                for (int b = 0; b < DBLK; ++b)
 #pragma unroll
-                for (int v = 0; v < 16; ++v) oacc[b][v] *= alpha;
+                    for (int v = 0; v < 16; ++v) oacc[b][v] *= alpha;
+            }
 
 #pragma unroll
             for (int c = 0; c < 4; ++c) {
