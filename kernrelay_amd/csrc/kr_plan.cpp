@@ -654,14 +654,35 @@ private:
     // when the GEMM ends and run better at full width. -1 (every tile waits
     // in-kernel) when PL is not one GEMM launch releasing every tile of its
     // node, or when the tail is small enough for the persistent grid.
+    // A GEMM released tile by tile runs co-resident tiles (room beside it
+    // for a consumer's waves) only where that costs it nothing: where its
+    // fastest tile is the 8-wave 256x256 kernel (every register of a CU) it
+    // runs that, its consumers wait in a one-wave kernel (5 registers, which
+    // fits beside it) and run at full width after it. Measured on the 4096^3
+    // mm -> {softmax, gelu, cast} fan-out: co-resident 256x128 tiles made
+    // the split 0.955x serial once the 256x256 kernel got faster.
+    // KR_PLAN_CORESIDENT=1 keeps co-resident tiles throughout.
+    bool CoresidentPays(const Launch &L) const
+    {
+        if (EnvInt("KR_PLAN_CORESIDENT", 0) != 0) return true;
+        const int64_t prows = L.pub_rows > 0 ? L.pub_rows : TaskRows(*L.task);
+        const int N = int(L.task->n_tile > 0 ? L.task->n_tile : L.node->n);
+        const GemmTile best = GemmPickTile(int(TaskRows(*L.task)), N, int(prows), false);
+        return !(best.bm == 256 && best.bn == 256);
+    }
+
     int EarlyTiles(const Launch &PL, const Launch &L, int64_t in_off, int64_t in_rows) const
     {
         const NodeSpec &P = *PL.node;
+        // a GEMM that leaves no room beside it: a persistent consumer grid
+        // would hold the CUs its own rows need, so its consumers take the
+        // one-wave wait kernel and run at full width after it
+        if (P.op == Op::MatMul && PL.publish && !PL.coresident) return 0;
         if (P.op != Op::MatMul || !PL.publish || PL.merged != NodeTiles(P) || PL.task->n_tile > 0) return -1;
         const int64_t prows = PL.pub_rows;
         if (prows <= 0 || L.tile_rows != prows || in_off % prows != 0) return -1;
         const int M = int(TaskRows(*PL.task)), N = int(P.n);
-        const GemmTile gt = GemmPickTile(M, N, int(prows), true);
+        const GemmTile gt = GemmPickTile(M, N, int(prows), PL.coresident);
         if (gt.bm <= 0) return -1;
         const int64_t tn = (N + gt.bn - 1) / gt.bn;
         const int64_t per = (prows / gt.bm) * tn;                 // workgroups per relay tile
@@ -769,17 +790,16 @@ private:
         Check(hipMemset(ctrl_.get(), 0, ctrl_words_ * 4), "zero ctrl");
         int32_t *ctrl = ctrl_.as<int32_t>();
 
+        // every producer's tile policy first: a consumer's early tiles follow it
+        for (Launch &L : launches_)
+            if (L.publish) L.coresident = L.node->op == Op::MatMul && CoresidentPays(L);
         for (size_t i = 0; i < launches_.size(); ++i) {
             Launch &L = launches_[i];
             const NodeSpec &n = *L.node;
             const TaskSpec &t = *L.task;
             const int64_t in_off = TaskInOff(t);
             const int64_t in_rows = TaskRows(t);
-            if (L.publish) {
-                L.flag = flag_base.at(n.id) + t.tile;
-                // a GEMM released tile by tile while a consumer spins beside it
-                L.coresident = n.op == Op::MatMul;
-            }
+            if (L.publish) L.flag = flag_base.at(n.id) + t.tile;
             if (sync_ == "event") {
                 if (L.publish) Check(hipEventCreateWithFlags(&L.pub_event, hipEventDisableTiming), "event");
                 continue;
