@@ -119,6 +119,13 @@ __device__ __forceinline__ int XcdChunk(int bid, int first, int per)
 __device__ __forceinline__ float FastExp(float x) { return __builtin_amdgcn_exp2f(x * 1.4426950408889634f); }
 __device__ __forceinline__ float FastRcp(float x) { return __builtin_amdgcn_rcpf(x); }
 
+// RoPE (rotate_half layout) of the pair (x1 in the first half of a head, x2
+// at the same offset in the second half), with cos / sin at the output
+// element's own position: first half x1*c - x2*s, second half x2*c + x1*s.
+// Explicit fmas, so the standalone kernel and the GEMM epilogue round alike.
+__device__ __forceinline__ float RopeFirst(float x1, float x2, float c, float s) { return __builtin_fmaf(x1, c, -(x2 * s)); }
+__device__ __forceinline__ float RopeSecond(float x2, float x1, float c, float s) { return __builtin_fmaf(x2, c, x1 * s); }
+
 // SiLU as every kernel here computes it (x * sigmoid(x)).
 __device__ __forceinline__ float Silu(float x) { return x * FastRcp(1.0f + FastExp(-x)); }
 

@@ -47,6 +47,15 @@ struct GemmDesc {
     size_t sk_ws_bytes = 0;
     int32_t *sk_cnt = nullptr;
     int sk_cnt_len = 0;
+    // RoPE epilogue: columns [0, rope_cols) of C are heads of rope_d (64 or
+    // 128) values rotated after the bias, as the standalone RoPE kernel
+    // rotates the stored product (row r at position rope_pos0 + r; tables
+    // [positions, rope_d]). rope_cols % rope_d == 0.
+    const void *rope_cos = nullptr;
+    const void *rope_sin = nullptr;
+    int rope_cols = 0;
+    int rope_d = 0;
+    int rope_pos0 = 0;
     int order_rows = 0;          // > 0: produce in runs of this many rows (a
                                  // multiple of pub.rows_per_tile), default
                                  // one run per relay tile

@@ -61,6 +61,9 @@ struct GemmParams {
     int32_t *sk_cnt;     // [tiles] arrival counters, zero between launches
     int gemm_wgs;        // workgroups of the GEMM proper; the rest are tail
     int tail_wpt;        // tail workgroups per relay tile
+    const uint16_t *rope_cos;  // RoPE epilogue (nullptr: none)
+    const uint16_t *rope_sin;
+    int rope_cols, rope_d, rope_pos0;
 };
 
 __device__ __forceinline__ int Swz(int row, int chunk) { return chunk ^ ((row >> 1) & 7); }
@@ -258,8 +261,36 @@ __device__ __forceinline__ void StoreTile(const GemmParams &p, f32x16 (&acc)[MI]
         const int gm = m0 + row;
         const int gn = n0 + ch * 8;
         if (gm >= p.M || gn >= p.N) continue;
-        uint4 v = *reinterpret_cast<const uint4 *>(stage + row * BN + (ch ^ ((row & 31) >> 1)) * 8);
-        if (row & 1) v = make_uint4(v.z, v.w, v.x, v.y);
+        auto staged = [&](int c) {
+            uint4 u = *reinterpret_cast<const uint4 *>(stage + row * BN + (c ^ ((row & 31) >> 1)) * 8);
+            return (row & 1) ? make_uint4(u.z, u.w, u.x, u.y) : u;
+        };
+        uint4 v = staged(ch);
+        if (p.rope_cos != nullptr && gn < p.rope_cols) {
+            // the partner half of the head is in this tile (tiles start on
+            // head boundaries: BN and n0 are multiples of rope_d)
+            const int d0 = gn % p.rope_d, half = p.rope_d / 2;
+            const uint4 w = staged(d0 < half ? ch + half / 8 : ch - half / 8);
+            const int64_t t = int64_t(p.rope_pos0 + gm) * p.rope_d + d0;
+            const U16x8 c8 = LoadU16x8(p.rope_cos + t), s8 = LoadU16x8(p.rope_sin + t);
+            const uint32_t xv[4] = {v.x, v.y, v.z, v.w}, wv[4] = {w.x, w.y, w.z, w.w};
+            uint32_t o[4];
+#pragma unroll
+            for (int e2 = 0; e2 < 4; ++e2) {
+                uint32_t pair = 0;
+#pragma unroll
+                for (int h = 0; h < 2; ++h) {
+                    const int e = 2 * e2 + h;
+                    const float x = Elem<DT>::Load(uint16_t(xv[e2] >> (16 * h)));
+                    const float y = Elem<DT>::Load(uint16_t(wv[e2] >> (16 * h)));
+                    const float c = Elem<DT>::Load(c8.v[e]), sn = Elem<DT>::Load(s8.v[e]);
+                    const float r = d0 < half ? RopeFirst(x, y, c, sn) : RopeSecond(x, y, c, sn);
+                    pair |= uint32_t(Elem<DT>::Store(r)) << (16 * h);
+                }
+                o[e2] = pair;
+            }
+            v = make_uint4(o[0], o[1], o[2], o[3]);
+        }
         uint16_t *dst = p.C + int64_t(gm) * p.ldc + gn;
         if (vec && gn + 8 <= p.N) {
             if (!coh && p.store_kind == 2) {
@@ -765,6 +796,20 @@ void GemmLaunch(const GemmDesc &d, hipStream_t stream)
     p.tail_cols = d.tail_cols;
     p.epi_act = static_cast<uint16_t *>(d.epi_act);
     p.ld_act = d.ld_act;
+    if (d.rope_cos != nullptr) {
+        if (d.rope_sin == nullptr || (d.rope_d != 64 && d.rope_d != 128) || d.rope_cols <= 0 ||
+            d.rope_cols % d.rope_d != 0 || d.rope_cols > d.N || d.rope_pos0 < 0)
+            throw std::runtime_error("gemm: RoPE epilogue needs cos/sin tables, head size 64 or 128, whole heads");
+        if (p.epi_act != nullptr) throw std::runtime_error("gemm: RoPE and SwiGLU epilogues are exclusive");
+        if ((reinterpret_cast<uintptr_t>(d.rope_cos) | reinterpret_cast<uintptr_t>(d.rope_sin)) & 15)
+            throw std::runtime_error("gemm: RoPE tables must be 16-byte aligned");
+        // every tile width is a multiple of 128, so tiles start on head boundaries
+        p.rope_cos = static_cast<const uint16_t *>(d.rope_cos);
+        p.rope_sin = static_cast<const uint16_t *>(d.rope_sin);
+        p.rope_cols = d.rope_cols;
+        p.rope_d = d.rope_d;
+        p.rope_pos0 = d.rope_pos0;
+    }
     if (p.epi_act != nullptr) {
         if (p.tail_act != nullptr) throw std::runtime_error("gemm: SwiGLU epilogue and tail consumer are exclusive");
         if (d.dtype != kBF16 && d.dtype != kF16) throw std::runtime_error("gemm swiglu: 16-bit output only");

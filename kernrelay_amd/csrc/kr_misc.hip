@@ -60,8 +60,8 @@ __global__ void __launch_bounds__(256) RopeKernel(uint16_t *x, int64_t ld, int S
         for (int e = 0; e < 8; ++e) {
             const float x1 = Elem<DT>::Load(a.v[e]);
             const float x2 = Elem<DT>::Load(b.v[e]);
-            oa.v[e] = Elem<DT>::Store(x1 * Elem<DT>::Load(ca.v[e]) - x2 * Elem<DT>::Load(sa.v[e]));
-            ob.v[e] = Elem<DT>::Store(x2 * Elem<DT>::Load(cb.v[e]) + x1 * Elem<DT>::Load(sb.v[e]));
+            oa.v[e] = Elem<DT>::Store(RopeFirst(x1, x2, Elem<DT>::Load(ca.v[e]), Elem<DT>::Load(sa.v[e])));
+            ob.v[e] = Elem<DT>::Store(RopeSecond(x2, x1, Elem<DT>::Load(cb.v[e]), Elem<DT>::Load(sb.v[e])));
         }
         StoreU16x8(row + i0, oa);
         StoreU16x8(row + i1, ob);

@@ -633,6 +633,13 @@ private:
     void Gemm(int s, const void *A, int64_t lda, const uint16_t *Bt, int N, int K, void *C, int64_t ldc,
               const uint16_t *bias, int M, RelayPub pub, RelayWait wait = RelayWait{})
     {
+        const GemmDesc d = MakeGemm(A, lda, Bt, N, K, C, ldc, bias, M, pub, wait);
+        Emit(s, [d](hipStream_t st) { GemmLaunch(d, st); });
+    }
+
+    GemmDesc MakeGemm(const void *A, int64_t lda, const uint16_t *Bt, int N, int K, void *C, int64_t ldc,
+                      const uint16_t *bias, int M, RelayPub pub, RelayWait wait) const
+    {
         GemmDesc d;
         d.dtype = kBF16;
         d.A = A;
@@ -648,7 +655,7 @@ private:
         d.pub = pub;
         d.wait = wait;
         WithStreamK(d);
-        Emit(s, [d](hipStream_t st) { GemmLaunch(d, st); });
+        return d;
     }
 
     void AddRmsNorm(int s, const void *a, const void *b, const uint16_t *g, void *y, void *sum, RelayWait w,
@@ -727,7 +734,19 @@ private:
         const int S = seq_;
         const int64_t ld = ldqkv_;
         uint16_t *qkv = qkv_.as<uint16_t>();
-        Gemm(P, x_.get(), H_, w.qkv, int(ld), H_, qkv, ld, w.bias, S, RelayPub{}, qkv_wait);
+        // without q/k norms RoPE rides in the QKV GEMM's epilogue (the
+        // standalone kernel's arithmetic on the bias-added product): the q and
+        // k columns never make a second pass (KR_QWEN_ROPE_EPI=0: separate)
+        const bool rope_epi = !qk_norm_ && EnvInt("KR_QWEN_ROPE_EPI", 1) != 0;
+        GemmDesc gd = MakeGemm(x_.get(), H_, w.qkv, int(ld), H_, qkv, ld, w.bias, S, RelayPub{}, qkv_wait);
+        if (rope_epi) {
+            gd.rope_cos = cos_;
+            gd.rope_sin = sin_;
+            gd.rope_cols = (HQ_ + HKV_) * D_;
+            gd.rope_d = D_;
+            gd.rope_pos0 = 0;
+        }
+        Emit(P, [gd](hipStream_t st) { GemmLaunch(gd, st); });
         uint16_t *q = qkv, *kk = qkv + size_t(HQ_) * D_, *v = qkv + size_t(HQ_ + HKV_) * D_;
         int64_t ldq = ld, ldk = ld;
         if (qk_norm_) {
@@ -740,10 +759,12 @@ private:
         }
         const int HQ = HQ_, HKV = HKV_, D = D_;
         const uint16_t *cs = cos_, *sn = sin_;
-        Emit(P, [=](hipStream_t st) {
-            RopeLaunch(kBF16, q, ldq, S, HQ, D, cs, sn, st);
-            RopeLaunch(kBF16, kk, ldk, S, HKV, D, cs, sn, st);
-        });
+        if (!rope_epi) {
+            Emit(P, [=](hipStream_t st) {
+                RopeLaunch(kBF16, q, ldq, S, HQ, D, cs, sn, st);
+                RopeLaunch(kBF16, kk, ldk, S, HKV, D, cs, sn, st);
+            });
+        }
         uint16_t *attn = attn_.as<uint16_t>();
         const float scale = float(1.0 / std::sqrt(double(D_)));
         Emit(P, [=](hipStream_t st) {

@@ -93,6 +93,31 @@ def test_split_k_down_all_modes_bit_exact(gpu, tmp_path):
         del os.environ["KR_QWEN_SPLITK"]
 
 
+@pytest.mark.parametrize("head_dim", [64, 128])
+def test_rope_epilogue_bit_exact(gpu, tmp_path, head_dim):
+    """RoPE in the QKV GEMM's epilogue (models without q/k norms) gives the
+    bits of the separate RoPE kernel: logits identical with and without it,
+    serial and relay split, for head sizes 64 and 128, and the oracle's."""
+    cfg = dict(modeldir.PRESETS["tiny-qwen2"])
+    cfg.update(hidden_size=512, num_attention_heads=4, num_key_value_heads=2, head_dim=head_dim)
+    seq = 512
+    d = modeldir.write_model_dir(tmp_path / ("rope%d" % head_dim), cfg, seq=seq)
+    ref = oq.write_reference(d)
+    fnv = {}
+    for epi in ("0", "1"):
+        os.environ["KR_QWEN_ROPE_EPI"] = epi
+        try:
+            for mode in ("graph_whole", "relay_split:4"):
+                dump = tmp_path / ("dump_%s_%s" % (epi, mode.replace(":", "_")))
+                dump.mkdir()
+                r = run(d, mode, seq, dump)
+                check_logits(dump, ref)
+                fnv[(epi, mode)] = r["logits_fnv64"]
+        finally:
+            del os.environ["KR_QWEN_ROPE_EPI"]
+    assert len(set(fnv.values())) == 1, fnv
+
+
 def test_qwen05_shapes_split_bit_exact(gpu, tmp_path):
     """Qwen2.5-0.5B layer shapes (H 896, 14/2 heads, D 64, I 4864, V 151936,
     tied) at seq 2048, two layers: serial == relay_split:4 (SwiGLU in the
