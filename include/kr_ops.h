@@ -172,6 +172,21 @@ int kr_op_attention(int dtype, const void *q, int64_t ldq, const void *k, int64_
                     const void *v, int64_t ldv, void *out, int64_t ldo, int S, int HQ, int HKV,
                     int D, float scale, void *stream);
 
+/* kr_op_attention with long causal rows split across workgroups: query
+ * blocks of more than 16 key blocks are cut into up to 4 pieces whose fp32
+ * partials the last piece sums in piece order (deterministic; the bits
+ * depend on S only). ws / counters of the sizes kr_op_attention_workspace
+ * reports (0 bytes: nothing to split, the call runs unsplit); counters zero
+ * before the first call and left zero by every call; calls sharing them must
+ * not overlap. Same role as kr_op_attention (reference
+ * exec/qwen_main.cpp:591-614, FlashN); the split is a scheduling choice of
+ * this build with no reference counterpart. */
+int kr_op_attention_workspace(int S, int HQ, int D, size_t *ws_bytes, int *counters);
+int kr_op_attention_split(int dtype, const void *q, int64_t ldq, const void *k, int64_t ldk,
+                          const void *v, int64_t ldv, void *out, int64_t ldo, int S, int HQ, int HKV,
+                          int D, float scale, void *ws, size_t ws_bytes, int32_t *counters,
+                          int n_counters, void *stream);
+
 /* dst[C,R] = src[R,C]^T for 16-bit elements (weight re-layout at load; the
  * reference stores matmul weights as weight_t [K,N], scripts/export_model.py:159-161). */
 int kr_op_transpose(const void *src, void *dst, int R, int C, void *stream);

@@ -23,6 +23,9 @@
 // Online softmax in base 2 (exponent fma(score, scale*log2(e), -m)), fp32
 // state, with the running max m moved lazily (see the loop).
 // Workgroups run heaviest (longest causal rows) first across all heads.
+#include <algorithm>
+#include <vector>
+
 #include "kr_misc.h"
 
 namespace kr {
@@ -36,6 +39,16 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 constexpr int kKvBlk = 64;
 constexpr int kQBlk = 128;
 
+// Work items, heaviest first: workgroup b runs item b / HQ of head b % HQ.
+// An item is query block qb over key blocks [kb_lo, kb_hi); a query block
+// whose causal row is long is cut into `pieces` items (split id sid), each
+// writing its fp32 partial (O, m, l); the last piece to finish sums them in
+// piece order.
+constexpr int kMaxItems = 128;
+struct AttnItem {
+    int16_t qb, kb_lo, kb_hi, piece, pieces, sid;
+};
+
 struct AttnParams {
     const uint16_t *q;
     const uint16_t *k;
@@ -44,6 +57,10 @@ struct AttnParams {
     int64_t ldq, ldk, ldv, ldo;  // row strides (elements) of the [S, heads*D] views
     int S, HQ, HKV;
     float scale_log2;
+    float *ws;       // split partials [sid][HQ][pmax][chunks][256 threads][4]
+    int32_t *cnt;    // [sid][HQ] arrival tickets, zero between launches
+    int pmax;
+    AttnItem items[kMaxItems];
 };
 
 template <int DT>
@@ -80,13 +97,14 @@ __global__ void __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_wav
     __shared__ __attribute__((aligned(16))) uint16_t Ks[2][kKvBlk * D];
     __shared__ __attribute__((aligned(16))) uint16_t Vt[2][D * kKvBlk];
 
+    __shared__ int last_piece;
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
     const int hf = lane >> 5;
-    const int nqb = (p.S + kQBlk - 1) / kQBlk;
     const int h = int(blockIdx.x) % p.HQ;
-    const int qb = nqb - 1 - int(blockIdx.x) / p.HQ;  // longest causal rows first, all heads
+    const AttnItem item = p.items[int(blockIdx.x) / p.HQ];
+    const int qb = item.qb;
     const int q0 = qb * kQBlk;
     const int kvh = h / (p.HQ / p.HKV);
     const int64_t ldq = p.ldq;
@@ -111,8 +129,7 @@ __global__ void __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_wav
     float m = -INFINITY;
     float l = 0.0f;
 
-    const int q_hi = min(q0 + kQBlk - 1, p.S - 1);
-    const int nkb = q_hi / kKvBlk + 1;
+    const int kb_lo = item.kb_lo, kb_hi = item.kb_hi;
 
     // block kb -> registers (rows past S read as zero)
     uint4 kr[KL];
@@ -170,14 +187,14 @@ __global__ void __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_wav
         }
     };
 
-    load(0);
+    load(kb_lo);
     store(0);
     __syncthreads();
 
-    for (int kb = 0; kb < nkb; ++kb) {
+    for (int kb = kb_lo; kb < kb_hi; ++kb) {
         const int kv0 = kb * kKvBlk;
-        const int cur = kb & 1;
-        const bool more = kb + 1 < nkb;
+        const int cur = (kb - kb_lo) & 1;
+        const bool more = kb + 1 < kb_hi;
         if (more) load(kb + 1);
 
         if (kv0 <= wave_q_hi) {  // else: block entirely in this wave's future
@@ -263,6 +280,58 @@ __global__ void __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_wav
         __syncthreads();
     }
 
+    if (item.pieces > 1) {
+        // split row: every piece writes its partial (agent-scope stores,
+        // read back on any XCD); the last to arrive sums all of them in piece
+        // order, so the result does not depend on which piece finishes last
+        constexpr int NCH = DBLK * 4 + 1;  // 16-byte chunks per thread: O, then (m, l)
+        const int64_t slot0 = (int64_t(item.sid) * p.HQ + h) * p.pmax;
+        auto part = [&](int piece, int ch, int e) {
+            return p.ws + (((slot0 + piece) * NCH + ch) * 256 + tid) * 4 + e;
+        };
+#pragma unroll
+        for (int b = 0; b < DBLK; ++b)
+#pragma unroll
+            for (int v = 0; v < 16; ++v)
+                __hip_atomic_store(part(item.piece, b * 4 + v / 4, v % 4), oacc[b][v], __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(part(item.piece, NCH - 1, 0), m, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(part(item.piece, NCH - 1, 1), l, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this thread's partial is written
+        __syncthreads();
+        if (tid == 0) {
+            int32_t *c = p.cnt + int64_t(item.sid) * p.HQ + h;
+            const int32_t t = __hip_atomic_fetch_add(c, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            last_piece = t == item.pieces - 1;
+            if (last_piece) __hip_atomic_store(c, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        __syncthreads();
+        if (!last_piece) return;
+        float mp[4], lp[4];
+        float mall = -INFINITY;
+        for (int q = 0; q < item.pieces; ++q) {
+            mp[q] = __hip_atomic_load(part(q, NCH - 1, 0), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            lp[q] = __hip_atomic_load(part(q, NCH - 1, 1), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            mall = fmaxf(mall, mp[q]);
+        }
+        const float msub = mall == -INFINITY ? 0.0f : mall;
+#pragma unroll
+        for (int b = 0; b < DBLK; ++b)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) oacc[b][v] = 0.0f;
+        l = 0.0f;
+        for (int q = 0; q < item.pieces; ++q) {
+            const float a = __builtin_amdgcn_exp2f(mp[q] - msub);  // 0 for an empty piece (m = -inf)
+            l = __builtin_fmaf(lp[q], a, l);
+#pragma unroll
+            for (int b = 0; b < DBLK; ++b)
+#pragma unroll
+                for (int v = 0; v < 16; ++v)
+                    oacc[b][v] = __builtin_fmaf(
+                        __hip_atomic_load(part(q, b * 4 + v / 4, v % 4), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT), a,
+                        oacc[b][v]);
+        }
+    }
     l += __shfl_xor(l, 32, 64);
     const float inv = l > 0.0f ? 1.0f / l : 0.0f;
     if (qrow < p.S) {
@@ -284,8 +353,80 @@ __global__ void __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_wav
 
 }  // namespace
 
+namespace {
+
+// Split plan: query block qb covers key blocks [0, nkb(qb)); rows longer than
+// `cap` key blocks are cut into ceil(nkb / cap) pieces (at most 4), so no
+// workgroup carries far more than the average and the grid's critical path
+// shrinks. Items are ordered heaviest first.
+struct AttnPlan {
+    std::vector<AttnItem> items;
+    int nsplit = 0, pmax = 1;
+};
+
+int AttnCap()
+{
+    static const int v = [] {
+        const char *e = std::getenv("KR_ATTN_CAP");
+        return e != nullptr ? std::max(1, std::atoi(e)) : 16;
+    }();
+    return v;
+}
+
+AttnPlan PlanAttn(int S, bool split)
+{
+    AttnPlan pl;
+    const int nqb = (S + kQBlk - 1) / kQBlk;
+    for (int qb = 0; qb < nqb; ++qb) {
+        const int q_hi = std::min(qb * kQBlk + kQBlk - 1, S - 1);
+        const int nkb = q_hi / kKvBlk + 1;
+        const int pieces = split ? std::min(4, (nkb + AttnCap() - 1) / AttnCap()) : 1;
+        const int sid = pieces > 1 ? pl.nsplit++ : 0;
+        pl.pmax = std::max(pl.pmax, pieces);
+        for (int pc = 0; pc < pieces; ++pc)
+            pl.items.push_back({int16_t(qb), int16_t(nkb * pc / pieces), int16_t(nkb * (pc + 1) / pieces), int16_t(pc),
+                                int16_t(pieces), int16_t(sid)});
+    }
+    std::stable_sort(pl.items.begin(), pl.items.end(), [](const AttnItem &a, const AttnItem &b) {
+        const int wa = a.kb_hi - a.kb_lo, wb = b.kb_hi - b.kb_lo;
+        return wa != wb ? wa > wb : a.qb > b.qb;
+    });
+    return pl;
+}
+
+}  // namespace
+
+// Resident workgroup slots of the device (two 256-thread workgroups per CU).
+int AttnSlots()
+{
+    static const int v = [] {
+        int dev = 0, n = 0;
+        if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+            n = 256;
+        return 2 * std::max(n, 1);
+    }();
+    return v;
+}
+
+void AttnSplitNeeds(int S, int HQ, int D, size_t *ws_bytes, int *counters)
+{
+    *ws_bytes = 0;
+    *counters = 0;
+    if (S <= 0 || HQ <= 0 || (D != 64 && D != 128)) return;
+    // Split only a grid that leaves half the resident slots empty: a fuller
+    // grid is bound by the CUs' MFMA, softmax and LDS throughput, not by its
+    // longest row (measured on MI355X: 28 heads at S=2048 94 -> 116 us split,
+    // 14 heads 59 -> 49 us).
+    if (int64_t((S + kQBlk - 1) / kQBlk) * HQ * 2 > AttnSlots()) return;
+    const AttnPlan pl = PlanAttn(S, true);
+    if (pl.nsplit == 0 || pl.items.size() > size_t(kMaxItems)) return;
+    *ws_bytes = size_t(pl.nsplit) * HQ * pl.pmax * (D / 32 * 4 + 1) * 256 * 16;
+    *counters = pl.nsplit * HQ;
+}
+
 void AttnLaunch(int dtype, const void *q, int64_t ldq, const void *k, int64_t ldk, const void *v, int64_t ldv,
-                void *out, int64_t ldo, int S, int HQ, int HKV, int D, float scale, hipStream_t stream)
+                void *out, int64_t ldo, int S, int HQ, int HKV, int D, float scale, hipStream_t stream,
+                const AttnSplit *split)
 {
     if (S <= 0) return;
     if (HQ <= 0 || HKV <= 0 || HQ % HKV != 0) throw std::runtime_error("attention: HQ must be a multiple of HKV");
@@ -305,7 +446,19 @@ void AttnLaunch(int dtype, const void *q, int64_t ldq, const void *k, int64_t ld
     p.HQ = HQ;
     p.HKV = HKV;
     p.scale_log2 = scale * 1.4426950408889634f;
-    const dim3 grid(unsigned((S + kQBlk - 1) / kQBlk) * unsigned(HQ));
+    // split rows only with a workspace that holds the plan's partials
+    size_t need = 0;
+    int ncnt = 0;
+    if (split != nullptr) AttnSplitNeeds(S, HQ, D, &need, &ncnt);
+    const bool use_split = split != nullptr && need > 0 && split->ws != nullptr && split->cnt != nullptr &&
+                           split->ws_bytes >= need && split->cnt_len >= ncnt;
+    const AttnPlan pl = PlanAttn(S, use_split);
+    if (pl.items.size() > size_t(kMaxItems)) throw std::runtime_error("attention: sequence too long for the item table");
+    std::copy(pl.items.begin(), pl.items.end(), p.items);
+    p.ws = use_split ? split->ws : nullptr;
+    p.cnt = use_split ? split->cnt : nullptr;
+    p.pmax = pl.pmax;
+    const dim3 grid(unsigned(pl.items.size()) * unsigned(HQ));
     const bool bf = dtype == kBF16;
     if (dtype != kBF16 && dtype != kF16) throw std::runtime_error("attention: dtype must be bf16 or f16");
     if (D == 128) {

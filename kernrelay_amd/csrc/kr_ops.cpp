@@ -251,6 +251,26 @@ int kr_op_attention(int dtype, const void *q, int64_t ldq, const void *k, int64_
     return Guard([&] { kr::AttnLaunch(dtype, q, ldq, k, ldk, v, ldv, out, ldo, S_, HQ, HKV, D, scale, S(stream)); });
 }
 
+int kr_op_attention_workspace(int S_, int HQ, int D, size_t *ws_bytes, int *counters)
+{
+    if (ws_bytes == nullptr || counters == nullptr) return 2;
+    return Guard([&] { kr::AttnSplitNeeds(S_, HQ, D, ws_bytes, counters); });
+}
+
+int kr_op_attention_split(int dtype, const void *q, int64_t ldq, const void *k, int64_t ldk, const void *v,
+                          int64_t ldv, void *out, int64_t ldo, int S_, int HQ, int HKV, int D, float scale, void *ws,
+                          size_t ws_bytes, int32_t *counters, int n_counters, void *stream)
+{
+    return Guard([&] {
+        kr::AttnSplit sp;
+        sp.ws = static_cast<float *>(ws);
+        sp.ws_bytes = ws_bytes;
+        sp.cnt = counters;
+        sp.cnt_len = n_counters;
+        kr::AttnLaunch(dtype, q, ldq, k, ldk, v, ldv, out, ldo, S_, HQ, HKV, D, scale, S(stream), &sp);
+    });
+}
+
 int kr_op_transpose(const void *src, void *dst, int R, int C, void *stream)
 {
     return Guard([&] { kr::TransposeLaunch(src, dst, R, C, S(stream)); });

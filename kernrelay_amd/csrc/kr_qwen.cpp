@@ -541,6 +541,23 @@ private:
                 skcnt_len_ = std::max(skcnt_len_, c);
             }
         }
+        // attention: long causal rows split across workgroups (every mode
+        // runs the same split; KR_QWEN_ATTN_SPLIT=0 keeps one workgroup per
+        // query block)
+        if (EnvInt("KR_QWEN_ATTN_SPLIT", 1) != 0) {
+            size_t b = 0;
+            int c = 0;
+            AttnSplitNeeds(seq_, HQ_, D_, &b, &c);
+            if (b > 0) {
+                attn_ws_.Alloc(b);
+                attn_cnt_.Alloc(size_t(c) * 4);
+                Check(hipMemset(attn_cnt_.get(), 0, attn_cnt_.bytes()), "zero attention counters");
+                attn_split_.ws = attn_ws_.as<float>();
+                attn_split_.ws_bytes = b;
+                attn_split_.cnt = attn_cnt_.as<int32_t>();
+                attn_split_.cnt_len = c;
+            }
+        }
         if (skws_bytes_ > 0) {
             skws_.Alloc(skws_bytes_);
             skcnt_.Alloc(size_t(skcnt_len_) * 4);
@@ -767,8 +784,10 @@ private:
         }
         uint16_t *attn = attn_.as<uint16_t>();
         const float scale = float(1.0 / std::sqrt(double(D_)));
+        const AttnSplit sp = attn_split_;
         Emit(P, [=](hipStream_t st) {
-            AttnLaunch(kBF16, q, ldq, kk, ldk, v, ld, attn, int64_t(HQ) * D, S, HQ, HKV, D, scale, st);
+            AttnLaunch(kBF16, q, ldq, kk, ldk, v, ld, attn, int64_t(HQ) * D, S, HQ, HKV, D, scale, st,
+                       sp.ws != nullptr ? &sp : nullptr);
         });
     }
 
@@ -1030,6 +1049,8 @@ private:
     std::vector<std::pair<hipGraph_t, hipGraphExec_t>> graphs_;
     DevBuf ctrl_;
     DevBuf skws_, skcnt_;  // stream-K partials and tile counters
+    DevBuf attn_ws_, attn_cnt_;  // attention split partials and tickets
+    AttnSplit attn_split_{};
     size_t skws_bytes_ = 0;
     int skcnt_len_ = 0;
     size_t ctrl_blocks_ = 0;

@@ -48,6 +48,10 @@ def _lib():
         L.kr_op_embedding.argtypes = [vp, vp, vp, i32, i32, i64, vp]
         L.kr_op_rope.argtypes = [i32, vp, i64, i32, i32, i32, vp, vp, vp]
         L.kr_op_attention.argtypes = [i32, vp, i64, vp, i64, vp, i64, vp, i64, i32, i32, i32, i32, f32, vp]
+        L.kr_op_attention_workspace.argtypes = [i32, i32, i32, ctypes.POINTER(ctypes.c_size_t),
+                                                ctypes.POINTER(ctypes.c_int)]
+        L.kr_op_attention_split.argtypes = [i32, vp, i64, vp, i64, vp, i64, vp, i64, i32, i32, i32, i32, f32, vp,
+                                            ctypes.c_size_t, vp, i32, vp]
         L.kr_op_transpose.argtypes = [vp, vp, i32, i32, vp]
         L.kr_op_gemm_swiglu.argtypes = [i32, vp, i64, vp, i64, vp, vp, i32, i32, i32, ctypes.POINTER(KrPub),
                                         i32, i32, vp]
@@ -62,7 +66,8 @@ def _lib():
         L.kr_op_stream_destroy.restype = ctypes.c_int
         for name in ("kr_op_gemm", "kr_op_gemm_swiglu", "kr_op_gemm_swiglu_epilogue", "kr_op_gemm_streamk",
                      "kr_op_gemm_streamk_workspace", "kr_op_elementwise", "kr_op_rowop", "kr_op_wait", "kr_op_publish",
-                     "kr_op_embedding", "kr_op_rope", "kr_op_attention", "kr_op_transpose"):
+                     "kr_op_embedding", "kr_op_rope", "kr_op_attention", "kr_op_attention_workspace",
+                     "kr_op_attention_split", "kr_op_transpose"):
             getattr(L, name).restype = ctypes.c_int
         _BOUND = True
     return L
@@ -216,6 +221,22 @@ def attention(q, k, v, out, S, HQ, HKV, D, scale=None, ldq=0, ldk=0, ldv=0, ldo=
     scale = scale if scale is not None else D ** -0.5
     _check(_lib().kr_op_attention(_dt(q), _ptr(q), ldq, _ptr(k), ldk, _ptr(v), ldv, _ptr(out), ldo,
                                   S, HQ, HKV, D, float(scale), _stream(stream)))
+
+
+def attention_workspace(S, HQ, D):
+    """(workspace bytes, counters) attention_split needs; (0, 0) when no query
+    row is long enough to split."""
+    b, c = ctypes.c_size_t(0), ctypes.c_int(0)
+    _check(_lib().kr_op_attention_workspace(S, HQ, D, ctypes.byref(b), ctypes.byref(c)))
+    return b.value, c.value
+
+
+def attention_split(q, k, v, out, S, HQ, HKV, D, ws, counters, scale=None, ldq=0, ldk=0, ldv=0, ldo=0,
+                    stream=None):
+    scale = scale if scale is not None else D ** -0.5
+    _check(_lib().kr_op_attention_split(_dt(q), _ptr(q), ldq, _ptr(k), ldk, _ptr(v), ldv, _ptr(out), ldo,
+                                        S, HQ, HKV, D, float(scale), _ptr(ws), ws.numel() * ws.element_size(),
+                                        _ptr(counters), counters.numel(), _stream(stream)))
 
 
 def transpose(src, dst, stream=None):

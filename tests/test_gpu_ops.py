@@ -233,6 +233,44 @@ def test_attention(gpu, S, HQ, HKV, D):
     close(out, O.attention(q.float(), k.float(), v.float()))
 
 
+@pytest.mark.parametrize("S,HQ,HKV,D", [(2048, 14, 2, 64), (1500, 3, 1, 128), (4096, 4, 2, 64), (1100, 2, 2, 64)])
+def test_attention_split(gpu, S, HQ, HKV, D):
+    """Long causal rows split across workgroups (query blocks of more than 16
+    key blocks: two to four pieces summed in piece order by the last piece):
+    matches the oracle and the unsplit kernel within the bf16 bar, repeats bit
+    for bit, leaves its counters zero."""
+    announce("attention split S=%d HQ=%d HKV=%d D=%d" % (S, HQ, HKV, D))
+    nbytes, ncnt = ops.attention_workspace(S, HQ, D)
+    assert nbytes > 0 and ncnt > 0
+    q = rand((S, HQ, D), 1.0, 30).cuda()
+    k = rand((S, HKV, D), 1.0, 31).cuda()
+    v = rand((S, HKV, D), 1.0, 32).cuda()
+    ws = torch.empty(nbytes, dtype=torch.uint8, device="cuda")
+    cnt = torch.zeros(ncnt, dtype=torch.int32, device="cuda")
+    out = torch.empty(S, HQ, D, dtype=torch.bfloat16, device="cuda")
+    ops.attention_split(q, k, v, out, S, HQ, HKV, D, ws, cnt)
+    first = out.clone()
+    for _ in range(2):
+        out.zero_()
+        ops.attention_split(q, k, v, out, S, HQ, HKV, D, ws, cnt)
+        torch.cuda.synchronize()
+        assert torch.equal(out, first)
+    assert int(cnt.abs().sum()) == 0
+    plain = torch.empty_like(out)
+    ops.attention(q, k, v, plain, S, HQ, HKV, D)
+    close(out, plain)
+    close(out, O.attention(q.cpu().float(), k.cpu().float(), v.cpu().float()))
+
+
+def test_attention_split_workspace():
+    """Nothing to split at or below 16 key blocks per query row, nor when the
+    unsplit grid fills more than half of the resident slots (2 per CU)."""
+    assert ops.attention_workspace(1024, 14, 64) == (0, 0)
+    assert ops.attention_workspace(2048, 28, 128) == (0, 0)
+    b, c = ops.attention_workspace(2048, 14, 64)
+    assert c == 8 * 14 and b == 8 * 14 * 2 * 9 * 256 * 16
+
+
 def test_attention_strided_views(gpu):
     """q/k/v read in place from one fused [S, (HQ+2HKV)*D] buffer."""
     announce("attention strided")
