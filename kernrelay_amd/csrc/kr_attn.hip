@@ -178,11 +178,14 @@ __global__ void __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_wav
 #pragma unroll
             for (int e = 0; e < 8; ++e) {
                 const int d = c * 8 + e;
-                const int sh = (e & 1) * 16;
-                const uint32_t k0 = (w0[e >> 1] >> sh) & 0xffffu, k1 = (w1[e >> 1] >> sh) & 0xffffu;
-                const uint32_t k2 = (w2[e >> 1] >> sh) & 0xffffu, k3 = (w3[e >> 1] >> sh) & 0xffffu;
+                // the 16-bit halves e&1 of keys (0, 1) and (2, 3), paired by
+                // one byte permute each: v_perm_b32(hi, lo, sel) picks bytes
+                // of the 64-bit {hi, lo}, sel 0x05040100 = low halves,
+                // 0x07060302 = high halves
+                const uint32_t sel = (e & 1) ? 0x07060302u : 0x05040100u;
                 *reinterpret_cast<uint2 *>(&Vt[b][d * kKvBlk + (((u >> 1) ^ VSwz(d)) * 8) + (u & 1) * 4]) =
-                    make_uint2(k0 | (k1 << 16), k2 | (k3 << 16));
+                    make_uint2(__builtin_amdgcn_perm(w1[e >> 1], w0[e >> 1], sel),
+                               __builtin_amdgcn_perm(w3[e >> 1], w2[e >> 1], sel));
             }
         }
     };
