@@ -26,6 +26,7 @@ sys.path.insert(0, str(ROOT))
 PEAK_BF16_TFLOPS = 2500.0     # MI355X dense bf16 MFMA peak (vendor figure, no sparsity)
 PEAK_HBM_GBS = 8000.0
 REF_BEST_TOK_S = 2048 / 0.1462  # reference graph_whole, Qwen2.5-7B seq 2048, Ascend 910B3 (RESULTS.md:21)
+PRESET_NAMES = {"qwen2.5-7b": "Qwen2.5-7B", "qwen2.5-0.5b": "Qwen2.5-0.5B", "qwen3-8b": "Qwen3-8B"}
 
 
 def log(msg):
@@ -241,10 +242,13 @@ def main():
             "value": round(value, 1), "unit": "tok/s", "n_gpus": 1, "steps": args.steps,
             "warmup": args.warmup, "ms_per_step": round(total_split_s * 1e3 / args.steps, 3),
             "higher_is_better": True, "scaling": "weak",
-            "vs_baseline": round(value / REF_BEST_TOK_S, 3), "dtype": "bf16",
+            # the published reference number is for the 7B model at seq 2048
+            "vs_baseline": round(value / REF_BEST_TOK_S, 3) if (args.preset, S) == ("qwen2.5-7b", 2048) else None,
+            "dtype": "bf16",
             "data": "synthetic (random-init N(0,0.02) bf16 weights, uniform token ids)",
-            "config": {"workload": "Qwen2.5-7B-shaped prefill, batch 1, seq %d, relay split %d tiles"
-                       % (S, args.tiles), "model": args.preset, "global_batch": 1, "seq_len": S,
+            "config": {"workload": "%s-shaped prefill, batch 1, seq %d, relay split %d tiles"
+                       % (PRESET_NAMES.get(args.preset, args.preset), S, args.tiles), "model": args.preset,
+                       "global_batch": 1, "seq_len": S,
                        "parallelism": "none (1 GPU)", "tiles": args.tiles},
             "serial_ms_per_step": round(total_serial_s * 1e3 / args.steps, 3),
             "serial_tok_s": round(args.steps * S / total_serial_s, 1),

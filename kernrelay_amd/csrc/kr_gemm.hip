@@ -621,16 +621,21 @@ int CuCount()
     return v;
 }
 
-// Stream-K plan of a GEMM whose 256x256 tiles leave CUs idle. Default: an
-// exact split of K, S = CUs / tiles pieces per tile (S >= 2), capped so that
-// every piece keeps at least 64 K stages (shorter pieces do not repay the
-// fp32 partials and the fix-up), so every workgroup runs one piece and the
-// workgroups of an XCD walk K in step on a compact patch of tiles. Measured
-// on MI355X: down 2048x3584x18944 258 us (S = 2) against 288 us for the best
-// data-parallel tiles; spreading the iterations over all 256 CUs instead
-// (pieces of uneven length, two or three per tile at different K offsets,
-// sharing no operand lines) took 369 us. KR_GEMM_SK_WGS=G forces that even
-// spread over G workgroups (a measurement aid).
+// Stream-K plan of a GEMM whose data-parallel tiling leaves CUs idle.
+// Default: an exact split of K over 256x256 tiles, S = CUs / tiles pieces per
+// tile, each piece at least 16 K stages (S >= 2), so every workgroup runs one
+// piece and the workgroups of an XCD walk K in step on a compact patch of
+// tiles; only where the best data-parallel tiling fills less than 60% of the
+// device's workgroup slots. The last piece to finish sums all S partials
+// alone, so short pieces lose to that fix-up. Measured on MI355X with a warm
+// activation: 2048x896x4864 data-parallel 67.1 us (best tile), 2 pieces 65.7,
+// 4 pieces (19 stages) 53.6, 8 pieces (9.5 stages) 78.2; 2048x896x896 with 2
+// pieces of 7 stages 32.3 against 21.0; 2048x3584x18944 (the data-parallel
+// 256x128 tiles fill 87.5%) stays data-parallel: 245 us against 257 us split
+// in the prefill. Spreading the iterations of every tile over all 256 CUs
+// instead (pieces of uneven length at different K offsets, sharing no
+// operand lines) took 369 us for 2048x3584x18944. KR_GEMM_SK_WGS=G forces that
+// even spread over G workgroups (a measurement aid).
 bool PlanStreamK(int M, int N, int K, StreamKPlan &pl)
 {
     if (K % kPipeK != 0 || M < 256 || N < 256) return false;
@@ -640,7 +645,12 @@ bool PlanStreamK(int M, int N, int K, StreamKPlan &pl)
         pl.G = std::max(1, std::atoi(e));
         if (pl.tiles >= pl.G || int64_t(pl.tiles) * pl.nk < 4 * int64_t(pl.G)) return false;
     } else {
-        const int S = std::min(CuCount() / pl.tiles, pl.nk / 64);
+        const GemmTile dp = GemmPickTile(M, N, 0, false);
+        const int dp_tiles = ((M + dp.bm - 1) / dp.bm) * ((N + dp.bn - 1) / dp.bn);
+        const int dp_slots = CuCount() * (dp.bm * dp.bn >= 256 * 128 ? 1 : 2);
+        const int dp_rounds = (dp_tiles + dp_slots - 1) / dp_slots;
+        if (double(dp_tiles) / (double(dp_rounds) * dp_slots) >= 0.6) return false;
+        const int S = std::min(CuCount() / pl.tiles, pl.nk / 16);
         if (S < 2) return false;
         pl.G = S * pl.tiles;
     }
@@ -735,10 +745,16 @@ GemmTile GemmPickTile(int M, int N, int relay_rows, bool coresident)
 {
     // Candidates from most to least data reuse; take the first that keeps the
     // device busy (>= 2 full waves of workgroups, or whole waves) or, failing
-    // that, the one with the best wave efficiency. Every tile runs the same MFMA and K order,
-    // so the choice never changes the arithmetic.
+    // that, the one with the best wave efficiency. A GEMM whose 128x128 tiles
+    // give every workgroup a CU of its own takes them: with so few workgroups
+    // each CU's load path is the limit, and smaller tiles put more CUs to work
+    // (MI355X, K 896: 2048x896 21.0 us against 24.0 for 128x256, 2048x1152
+    // 20.6 against 23.8). Every tile runs the same MFMA and K order, so the
+    // choice never changes the arithmetic.
     static const GemmTile cands[] = {{256, 256}, {256, 128}, {128, 256}, {128, 128}, {64, 256}};
     const int cus = 256;
+    if ((relay_rows == 0 || relay_rows % 128 == 0) && ((M + 127) / 128) * ((N + 127) / 128) <= cus)
+        return {128, 128};
     GemmTile best{-1, -1};
     double best_eff = -1.0;
     for (const GemmTile &t : cands) {

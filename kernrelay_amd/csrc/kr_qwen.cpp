@@ -521,16 +521,16 @@ private:
         a16(xf_, S * H_);
         a16(logits_, S * size_t(V_));
         rstd_.Alloc(S * 4);
-        // KR_QWEN_SPLITK=1: plain GEMMs split K over idle CUs where the
-        // GEMM planner finds an exact split (at seq 2048 the down projection,
-        // 2 pieces per tile). Off by default: in the prefill the down GEMM's
-        // input was just written and sits in the MALL, and data-parallel
-        // 256x128 tiles measured 245 us per launch against 257 us split
-        // (cold operands: 288 against 258). One workspace serves every plain
-        // GEMM (they run one after another on the producer stream), sized for
+        // Plain GEMMs split K over idle CUs where the GEMM planner finds an
+        // exact split (a data-parallel tiling that fills under 60% of the
+        // device and pieces of >= 16 K stages: the Qwen2.5-0.5B down
+        // projection, 4 pieces per tile; no 7B shape at seq 2048);
+        // KR_QWEN_SPLITK=0 turns it off. Every mode runs the same plan, so
+        // the modes stay bit-identical. One workspace serves every plain GEMM
+        // (they run one after another on the producer stream), sized for
         // whole-sequence and row-slice shapes; its tile counters start at
         // zero and every split GEMM leaves them at zero.
-        for (int k = 1; k <= 8 && EnvInt("KR_QWEN_SPLITK", 0) != 0; k *= 2) {
+        for (int k = 1; k <= 8 && EnvInt("KR_QWEN_SPLITK", 1) != 0; k *= 2) {
             const int M = seq_ / k;
             const int shapes[][2] = {{int(ldqkv_), H_}, {H_, HQ_ * D_}, {2 * I_, H_}, {I_, H_}, {H_, I_}, {int(V_), H_}};
             for (const auto &nk : shapes) {
@@ -566,7 +566,7 @@ private:
     }
 
     // Plain GEMMs may split K over idle CUs (GemmLaunch decides per shape;
-    // no workspace without KR_QWEN_SPLITK).
+    // no workspace with KR_QWEN_SPLITK=0).
     void WithStreamK(GemmDesc &d) const
     {
         if (skws_bytes_ == 0) return;
@@ -647,10 +647,14 @@ private:
         }
     }
 
+    // split_k = false for a GEMM that some program launches with an epilogue
+    // or tail that cannot split (the gate/up projection): every program must
+    // run the same K order for the same op.
     void Gemm(int s, const void *A, int64_t lda, const uint16_t *Bt, int N, int K, void *C, int64_t ldc,
-              const uint16_t *bias, int M, RelayPub pub, RelayWait wait = RelayWait{})
+              const uint16_t *bias, int M, RelayPub pub, RelayWait wait = RelayWait{}, bool split_k = true)
     {
-        const GemmDesc d = MakeGemm(A, lda, Bt, N, K, C, ldc, bias, M, pub, wait);
+        GemmDesc d = MakeGemm(A, lda, Bt, N, K, C, ldc, bias, M, pub, wait);
+        if (!split_k) d.streamk = false;
         Emit(s, [d](hipStream_t st) { GemmLaunch(d, st); });
     }
 
@@ -885,7 +889,8 @@ private:
                     if (tail_tiles > 0) {
                         Emit(P, [d](hipStream_t st) { GemmLaunch(d, st); });
                     } else {
-                        Gemm(P, x, H_, w.gu, 2 * I_, H_, gu_.get(), 2 * int64_t(I_), nullptr, S, RelayPub{});
+                        Gemm(P, x, H_, w.gu, 2 * I_, H_, gu_.get(), 2 * int64_t(I_), nullptr, S, RelayPub{},
+                             RelayWait{}, false);
                     }
                 });
                 if (tail_tiles < k) {
@@ -971,7 +976,8 @@ private:
             // gate/up -> SwiGLU
             WaitBefore(P, le[l].ln2_gu, k);
             Timed(P, [&] {
-                Gemm(P, x, H_, w.gu, 2 * I_, H_, gu_.get(), 2 * int64_t(I_), nullptr, S, release(le[l].gu_act));
+                Gemm(P, x, H_, w.gu, 2 * I_, H_, gu_.get(), 2 * int64_t(I_), nullptr, S, release(le[l].gu_act),
+                     RelayWait{}, false);
             });
             after(P, le[l].gu_act);
             {

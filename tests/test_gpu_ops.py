@@ -446,8 +446,9 @@ def test_gemm_swiglu_epilogue_bit_exact(gpu, M, I, K):
     close(act, O.swiglu(g[:, :, 0, :].reshape(M, I), g[:, :, 1, :].reshape(M, I)))
 
 
-@pytest.mark.parametrize("M,N,K,bias,wgs", [(2048, 3584, 18944, False, None), (1000, 2560, 16384, True, None),
-                                            (2048, 4608, 3584, True, 256), (2048, 3584, 3584, False, 256)])
+@pytest.mark.parametrize("M,N,K,bias,wgs", [(2048, 3584, 18944, False, 224), (1000, 2560, 16384, True, None),
+                                            (2048, 896, 4864, True, None), (2048, 4608, 3584, True, 256),
+                                            (2048, 3584, 3584, False, 256)])
 def test_gemm_streamk(gpu, M, N, K, bias, wgs):
     """Stream-K: the default exact split of K (the down shape: two pieces per
     tile; a ragged one: four) and, forced over 256 workgroups, the uneven
@@ -465,10 +466,14 @@ def test_gemm_streamk(gpu, M, N, K, bias, wgs):
 
 
 def test_gemm_streamk_policy(gpu):
-    """The default plan splits K only where whole pieces of >= 64 K stages
-    fill idle CUs: the down shape (112 tiles, 296 stages) splits in two, the
-    o and q/k/v shapes (56 stages) and a full-device shape do not."""
-    assert ops.gemm_streamk_workspace(2048, 3584, 18944) == (112 * 2 * 256 * 256 * 4, 112)
+    """The default plan splits K only where the data-parallel tiling fills
+    under 60% of the device and whole pieces of >= 16 K stages fill idle CUs:
+    2048x896x4864 (32 tiles of 76 stages) splits in four; the 7B shapes
+    (down's 256x128 tiles fill 87.5%, q/k/v's 144 tiles leave no room for a
+    second piece), short K (14 stages) and a full-device shape do not."""
+    assert ops.gemm_streamk_workspace(2048, 896, 4864) == (32 * 4 * 256 * 256 * 4, 32)
+    assert ops.gemm_streamk_workspace(2048, 896, 896) == (0, 0)
+    assert ops.gemm_streamk_workspace(2048, 3584, 18944) == (0, 0)
     assert ops.gemm_streamk_workspace(2048, 3584, 3584) == (0, 0)
     assert ops.gemm_streamk_workspace(2048, 4608, 3584) == (0, 0)
     assert ops.gemm_streamk_workspace(4096, 4096, 18944) == (0, 0)

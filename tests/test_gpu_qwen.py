@@ -36,12 +36,12 @@ def run(d, mode, seq, dump=None, iters=2):
     return r
 
 
-def check_logits(dump, ref):
+def check_logits(dump, ref, atol=2e-2):
     w = np.fromfile(dump / "last_logits_bf16.bin", dtype=np.uint16)
     g = torch.from_numpy(w.view(np.int16).copy()).view(torch.bfloat16).double()
     r = ref["last_logits"].double()
     err = (g - r).abs()
-    assert bool((err <= 2e-2 + 1e-2 * r.abs()).all()), float(err.max())
+    assert bool((err <= atol + 1e-2 * r.abs()).all()), float(err.max())
     if ref["margin"] > 4e-2:
         assert int(g.argmax()) == ref["argmax"]
 
@@ -64,12 +64,11 @@ def test_all_modes_bit_exact_and_match_oracle(gpu, tmp_path, preset):
 
 
 def test_split_k_down_all_modes_bit_exact(gpu, tmp_path):
-    """With KR_QWEN_SPLITK, layer shapes whose down projection splits K over
-    idle CUs (I 8192 at seq 512: 4 output tiles of 128 K stages, two pieces
-    each): every mode runs
-    the same split (relay_flag releases its relay tile from the split's
-    finishers), so the logits stay bit-identical across modes and match the
-    oracle."""
+    """Layer shapes whose down projection splits K over idle CUs (I 8192 at
+    seq 512: 4 output tiles of 128 K stages, eight pieces each; the gate/up
+    projection never splits): every mode runs the same split (relay_flag
+    releases its relay tile from the split's finishers), so the logits stay
+    bit-identical across modes and match the oracle."""
     from kernrelay_amd import ops
     cfg = dict(modeldir.PRESETS["tiny-qwen3"])
     cfg["intermediate_size"] = 8192
@@ -121,13 +120,18 @@ def test_rope_epilogue_bit_exact(gpu, tmp_path, head_dim):
 def test_qwen05_shapes_split_bit_exact(gpu, tmp_path):
     """Qwen2.5-0.5B layer shapes (H 896, 14/2 heads, D 64, I 4864, V 151936,
     tied) at seq 2048, two layers: serial == relay_split:4 (SwiGLU in the
-    gate/up epilogue, and flag-released), oracle argmax."""
+    gate/up epilogue, and flag-released), oracle argmax. The logit bound's
+    floor is 3e-2 here: the largest of 151936 bf16 logits' deviations from
+    the fp32 oracle measured 0.0234 on MI355X whether the down projection
+    splits K or not (mean 0.0039 both ways; 4 layers: 0.032 unsplit, 0.031
+    split), one bf16 step away from the 2e-2 floor of the 2048-entry
+    vocabularies."""
     seq = 2048
     d, ref = make(tmp_path, "qwen2.5-0.5b", seq, layers=2)
     dump = tmp_path / "dump"
     dump.mkdir()
     a = run(d, "graph_whole", seq, dump)
-    check_logits(dump, ref)
+    check_logits(dump, ref, atol=3e-2)
     b = run(d, "relay_split:4", seq)
     assert a["logits_fnv64"] == b["logits_fnv64"]
     assert b["flag_timeouts"] == 0
