@@ -707,7 +707,16 @@ void LaunchTyped(const GemmParams &base, int order_rows, int tail_tiles, hipStre
         grid_x += tail_tiles * p.tail_wpt;
     }
     const dim3 grid(grid_x);
-    if (p.K % kPipeK == 0 && !ForceSimple()) {
+    if constexpr (BM == 192) {
+        // 192x256: the 8-wave staged kernel only (GemmLaunch picks this tile
+        // only where that kernel runs)
+        static_assert(BN == 256, "192-row tiles pair with 256 columns");
+        if (sk != nullptr || p.K % kPipeK != 0 || ForceSimple() || MainLoopMode() != 2)
+            throw std::logic_error("gemm: 192x256 tiles run the staged kernel only");
+        hipLaunchKernelGGL((GemmPipeKernel<DT, BM, BN, 0, 8, false, 2>), grid, dim3(512), 0, stream, p);
+        Check(hipGetLastError(), "gemm launch");
+        return;
+    } else if (p.K % kPipeK == 0 && !ForceSimple()) {
         if constexpr (BM == 256 && BN == 256) {
             if (sk != nullptr) {
                 if (MainLoopMode() == 2) hipLaunchKernelGGL((GemmPipeKernel<DT, BM, BN, 0, 8, true, 2>), grid, dim3(512), 0, stream, p);
@@ -755,15 +764,29 @@ GemmTile GemmPickTile(int M, int N, int relay_rows, bool coresident)
     const int cus = 256;
     if ((relay_rows == 0 || relay_rows % 128 == 0) && ((M + 127) / 128) * ((N + 127) / 128) <= cus)
         return {128, 128};
+    // share of the device's slots the tiles' useful work fills
+    auto fill = [&](GemmTile t) {
+        const int tiles = ((M + t.bm - 1) / t.bm) * ((N + t.bn - 1) / t.bn);
+        const int slots = cus * (t.bm * t.bn >= 256 * 128 ? 1 : 2);
+        return double(M) * N / (double(Waves(tiles, slots)) * slots * t.bm * t.bn);
+    };
+    // 192x256 (three 32-row blocks per wave of the 8-wave grid) for a GEMM
+    // that 256x256 tiles leave a third idle and no smaller tile fills better,
+    // e.g. q/k/v 2048x4608: 198 tiles fill 75% against 144 tiles' 56%
+    // (without relay releases, waits or co-residency)
+    const bool try192 = relay_rows == 0 && !coresident;
     GemmTile best{-1, -1};
     double best_eff = -1.0;
+    auto pick192 = [&](GemmTile other) {
+        return try192 && fill({192, 256}) > 1.15 * fill(other) ? GemmTile{192, 256} : other;
+    };
     for (const GemmTile &t : cands) {
         if (relay_rows > 0 && relay_rows % t.bm != 0) continue;
         if (coresident && t.bm * t.bn >= 256 * 256) continue;
         const int tiles = ((M + t.bm - 1) / t.bm) * ((N + t.bn - 1) / t.bn);
         const int slots = cus * (t.bm * t.bn >= 256 * 128 ? 1 : 2);
         // enough workgroups for two rounds, or whole rounds exactly
-        if (tiles >= 2 * slots || tiles % slots == 0) return t;
+        if (tiles >= 2 * slots || tiles % slots == 0) return t.bm == 256 && t.bn == 256 ? t : pick192(t);
         const double work = double(t.bm) * t.bn;  // per-workgroup work unit
         const double eff = double(tiles) * work / (double(Waves(tiles, slots)) * slots * work);
         const double score = eff * (t.bm * t.bn >= 256 * 128 ? 1.0 : 0.85);
@@ -772,7 +795,7 @@ GemmTile GemmPickTile(int M, int N, int relay_rows, bool coresident)
             best = t;
         }
     }
-    return best;
+    return best.bm < 0 ? best : pick192(best);
 }
 
 void GemmStreamKNeeds(int M, int N, int K, size_t *ws_bytes, int *counters)
@@ -859,6 +882,11 @@ void GemmLaunch(const GemmDesc &d, hipStream_t stream)
     }
     if (t.bm < 0) throw std::runtime_error("gemm: relay tile rows must be a multiple of 64");
     if (d.epi_act != nullptr && t.bn < 256) t = {t.bm >= 256 ? 256 : 128, 256};  // the epilogue pairs 16-col groups
+    // 192x256 runs only on the staged 8-wave kernel; elsewhere 256x256 (the
+    // same MFMA and K order: the same bits)
+    if (t.bm == 192 && (d.K % kPipeK != 0 || ForceSimple() || MainLoopMode() != 2 || d.epi_act != nullptr ||
+                        d.tail_act != nullptr || d.pub.ctrl != nullptr || d.wait.ctrl != nullptr))
+        t = {256, 256};
     const bool bf = d.dtype == kBF16;
     if (d.dtype != kBF16 && d.dtype != kF16) throw std::runtime_error("gemm: dtype must be bf16 or f16");
     const int order = d.order_rows;
@@ -888,6 +916,7 @@ void GemmLaunch(const GemmDesc &d, hipStream_t stream)
         return;                                                                                    \
     }
     KR_GEMM_CASE(256, 256)
+    KR_GEMM_CASE(192, 256)
     KR_GEMM_CASE(256, 128)
     KR_GEMM_CASE(128, 256)
     KR_GEMM_CASE(128, 128)

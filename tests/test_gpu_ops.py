@@ -75,7 +75,7 @@ def test_gemm_tiles_bit_exact(gpu):
     A = rand((M, K), 1.0, 6).cuda()
     Bt = rand((N, K), 0.02, 7).cuda()
     outs = []
-    for bm in (256, 128, 64):
+    for bm in (256, 192, 128, 64):  # 192: three row blocks of 192 (the last 128 rows in bounds)
         C = torch.empty(M, N, dtype=torch.bfloat16, device="cuda")
         ops.gemm(A, Bt, C, bm=bm)
         outs.append(C)
@@ -87,6 +87,29 @@ def test_gemm_tiles_bit_exact(gpu):
     ops.gemm(A[256:384], Bt, C2)
     torch.cuda.synchronize()
     assert torch.equal(C2, outs[0][256:384])
+
+
+def test_gemm_192_rows_qkv_shape(gpu):
+    """The q/k/v projection shape 2048x4608x3584 (+bias) runs 192x256 tiles
+    (198 tiles fill 75% of the device against 144 256x256 tiles' 56%): the
+    same bits as 256x256 tiles, the oracle's values, nothing written outside
+    C; a ragged M (1000 rows: a partial last row block) too."""
+    announce("gemm 192x256 q/k/v shape")
+    for M in (2048, 1000):
+        N, K = 4608, 3584
+        A = rand((M, K), 1.0, 60).cuda()
+        Bt = rand((N, K), 0.02, 61).cuda()
+        b = rand((N,), 0.5, 62).cuda()
+        pad = torch.full((M + 4, N + 8), 5.0, dtype=torch.bfloat16, device="cuda")
+        C = pad[:M, :N]
+        ops.gemm(A, Bt, C, bias=b)
+        ref = torch.empty(M, N, dtype=torch.bfloat16, device="cuda")
+        ops.gemm(A, Bt, ref, bias=b, bm=256)
+        torch.cuda.synchronize()
+        assert torch.equal(C, ref)
+        assert torch.all(pad[M:] == 5.0) and torch.all(pad[:, N:] == 5.0)
+        rows = slice(0, M, 97)
+        close(C[rows].cpu(), O.gemm(A[rows].cpu(), Bt.cpu().t(), bias=b.cpu()))
 
 
 @pytest.mark.parametrize("op", ["gelu", "silu"])
