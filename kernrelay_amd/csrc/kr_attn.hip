@@ -37,6 +37,7 @@ typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 constexpr int kKvBlk = 64;
+typedef uint32_t AttnU32x4 __attribute__((ext_vector_type(4)));
 constexpr int kQBlk = 128;
 
 // Work items, heaviest first: workgroup b runs item b / HQ of head b % HQ.
@@ -131,28 +132,30 @@ __global__ void __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_wav
 
     const int kb_lo = item.kb_lo, kb_hi = item.kb_hi;
 
-    // block kb -> registers (rows past S read as zero)
-    uint4 kr[KL];
-    uint4 vr[VL][4];
+    // block kb -> registers, with no branch around a load: rows past S read
+    // row S-1 again (their keys are masked to -inf, so their P is exactly 0
+    // and their finite K and V rows contribute nothing), threads past the
+    // block's V groups (D 64) read group 0 again and never store it. Plain
+    // vector types: struct copies would go through memcpy, which keeps the
+    // arrays in scratch memory.
+    AttnU32x4 kr[KL];
+    AttnU32x4 vr[VL][4];
     auto load = [&](int kb) {
         const int kv0 = kb * kKvBlk;
 #pragma unroll
         for (int i = 0; i < KL; ++i) {
             const int t = tid + 256 * i;
-            const int kv = kv0 + t / DCH;
-            kr[i] = kv < p.S ? *reinterpret_cast<const uint4 *>(p.k + int64_t(kv) * p.ldk + int64_t(kvh) * D + (t % DCH) * 8)
-                             : make_uint4(0, 0, 0, 0);
+            const int kv = min(kv0 + t / DCH, p.S - 1);
+            kr[i] = *reinterpret_cast<const AttnU32x4 *>(p.k + int64_t(kv) * p.ldk + int64_t(kvh) * D + (t % DCH) * 8);
         }
 #pragma unroll
         for (int i = 0; i < VL; ++i) {
             const int t = tid + 256 * i;
-            const int grp = t / DCH, c = t % DCH;
+            const int grp = t < VG ? t / DCH : 0, c = t % DCH;
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                const int kv = kv0 + 4 * grp + r;
-                vr[i][r] = (t < VG && kv < p.S)
-                               ? *reinterpret_cast<const uint4 *>(p.v + int64_t(kv) * p.ldv + int64_t(kvh) * D + c * 8)
-                               : make_uint4(0, 0, 0, 0);
+                const int kv = min(kv0 + 4 * grp + r, p.S - 1);
+                vr[i][r] = *reinterpret_cast<const AttnU32x4 *>(p.v + int64_t(kv) * p.ldv + int64_t(kvh) * D + c * 8);
             }
         }
     };
@@ -163,18 +166,15 @@ __global__ void __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_wav
         for (int i = 0; i < KL; ++i) {
             const int t = tid + 256 * i;
             const int r = t / DCH, c = t % DCH;
-            *reinterpret_cast<uint4 *>(&Ks[b][r * D + KSwz<D>(r, c) * 8]) = kr[i];
+            *reinterpret_cast<AttnU32x4 *>(&Ks[b][r * D + KSwz<D>(r, c) * 8]) = kr[i];
         }
 #pragma unroll
         for (int i = 0; i < VL; ++i) {
             const int t = tid + 256 * i;
-            if (t >= VG) continue;
+            if (VG % 256 != 0 && t >= VG) continue;  // (D 64: half the threads)
             const int ap = t / DCH, c = t % DCH;  // keys 4ap..4ap+3, d chunk c
             const int u = 4 * (ap >> 2) + ((ap & 3) >> 1) + 2 * (ap & 1);  // 8-byte unit in the row
-            const uint32_t w0[4] = {vr[i][0].x, vr[i][0].y, vr[i][0].z, vr[i][0].w};
-            const uint32_t w1[4] = {vr[i][1].x, vr[i][1].y, vr[i][1].z, vr[i][1].w};
-            const uint32_t w2[4] = {vr[i][2].x, vr[i][2].y, vr[i][2].z, vr[i][2].w};
-            const uint32_t w3[4] = {vr[i][3].x, vr[i][3].y, vr[i][3].z, vr[i][3].w};
+            const AttnU32x4 &w0 = vr[i][0], &w1 = vr[i][1], &w2 = vr[i][2], &w3 = vr[i][3];
 #pragma unroll
             for (int e = 0; e < 8; ++e) {
                 const int d = c * 8 + e;
