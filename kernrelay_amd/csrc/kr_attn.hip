@@ -38,6 +38,20 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 constexpr int kKvBlk = 64;
 typedef uint32_t AttnU32x4 __attribute__((ext_vector_type(4)));
+
+// two values to 16 bits (round to nearest even, as Elem<DT>::Store), packed
+// low | high << 16: one v_cvt_pk_bf16_f32 for bf16
+template <int DT>
+__device__ __forceinline__ uint32_t Pack2(float lo, float hi)
+{
+    if constexpr (DT == kBF16) {
+        typedef float F2 __attribute__((ext_vector_type(2)));
+        typedef __bf16 B2 __attribute__((ext_vector_type(2)));
+        return __builtin_bit_cast(uint32_t, __builtin_convertvector((F2){lo, hi}, B2));
+    } else {
+        return uint32_t(Elem<DT>::Store(lo)) | (uint32_t(Elem<DT>::Store(hi)) << 16);
+    }
+}
 constexpr int kQBlk = 128;
 
 // Work items, heaviest first: workgroup b runs item b / HQ of head b % HQ.
@@ -140,8 +154,34 @@ __global__ void __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_wav
     // arrays in scratch memory.
     AttnU32x4 kr[KL];
     AttnU32x4 vr[VL][4];
+    // this thread's element offsets inside a block of K / V rows
+    int koff[KL], voff[VL][4];
+#pragma unroll
+    for (int i = 0; i < KL; ++i) {
+        const int t = tid + 256 * i;
+        koff[i] = (t / DCH) * int(p.ldk) + kvh * D + (t % DCH) * 8;
+    }
+#pragma unroll
+    for (int i = 0; i < VL; ++i) {
+        const int t = tid + 256 * i;
+        const int grp = t < VG ? t / DCH : 0, c = t % DCH;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) voff[i][r] = (4 * grp + r) * int(p.ldv) + kvh * D + c * 8;
+    }
     auto load = [&](int kb) {
         const int kv0 = kb * kKvBlk;
+        if (kv0 + kKvBlk <= p.S) {
+            // a whole block inside S: the block's base plus this thread's offsets
+            const uint16_t *kbase = p.k + int64_t(kv0) * p.ldk;
+            const uint16_t *vbase = p.v + int64_t(kv0) * p.ldv;
+#pragma unroll
+            for (int i = 0; i < KL; ++i) kr[i] = *reinterpret_cast<const AttnU32x4 *>(kbase + koff[i]);
+#pragma unroll
+            for (int i = 0; i < VL; ++i)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) vr[i][r] = *reinterpret_cast<const AttnU32x4 *>(vbase + voff[i][r]);
+            return;
+        }
 #pragma unroll
         for (int i = 0; i < KL; ++i) {
             const int t = tid + 256 * i;
@@ -253,7 +293,7 @@ __global__ void __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_wav
                 }
             l = l * alpha + lsum;
             m = mnew;
-            if (__builtin_amdgcn_read_exec() & __ballot(move)) {
+            if (__builtin_expect((__builtin_amdgcn_read_exec() & __ballot(move)) != 0, 0)) {
 #pragma unroll
                 for (int b = 0; b < DBLK; ++b)
 #pragma unroll
@@ -266,10 +306,7 @@ __global__ void __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_wav
                 const int vb = (c & 1) * 8;
                 uint32_t pw[4];
 #pragma unroll
-                for (int s = 0; s < 4; ++s) {
-                    pw[s] = uint32_t(Elem<DT>::Store(sacc[kh][vb + 2 * s])) |
-                            (uint32_t(Elem<DT>::Store(sacc[kh][vb + 2 * s + 1])) << 16);
-                }
+                for (int s = 0; s < 4; ++s) pw[s] = Pack2<DT>(sacc[kh][vb + 2 * s], sacc[kh][vb + 2 * s + 1]);
                 const uint4 pf = make_uint4(pw[0], pw[1], pw[2], pw[3]);
 #pragma unroll
                 for (int b = 0; b < DBLK; ++b) {
@@ -445,6 +482,9 @@ void AttnLaunch(int dtype, const void *q, int64_t ldq, const void *k, int64_t ld
     p.ldv = ldv > 0 ? ldv : int64_t(HKV) * D;
     p.ldo = ldo > 0 ? ldo : int64_t(HQ) * D;
     if ((p.ldq | p.ldk | p.ldv | p.ldo) % 8 != 0) throw std::runtime_error("attention: row strides must be multiples of 8");
+    // the kernel addresses K/V rows inside a 64-row block by 32-bit offsets
+    if (int64_t(std::max(p.ldk, p.ldv)) * 64 + int64_t(HKV) * D >= (int64_t(1) << 31))
+        throw std::runtime_error("attention: K/V row strides too large");
     p.S = S;
     p.HQ = HQ;
     p.HKV = HKV;
