@@ -74,6 +74,18 @@ def gemm_roofline(run, serial, S, N, K):
                                "note": "the serial program's plain gate/up GEMM (writes the [S, 2I] product)"}}
 
 
+def cpu_model():
+    """The host CPU's model name (/proc/cpuinfo), or the platform's."""
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    import platform
+    return platform.processor() or platform.machine()
+
+
 def cpu_baseline(model_dir, seconds_hint=20):
     """Oracle (fp32 torch CPU) on a bounded sample: decoder layer 0 and the
     lm_head over all rows at seq 2048; scaled to the full prefill as
@@ -102,7 +114,7 @@ def cpu_baseline(model_dir, seconds_hint=20):
         O.gemm(x, w)
         t_lm = time.perf_counter() - t0
     total = m.L * t_layer + t_lm
-    return {"value": round(S / total, 2), "unit": "tok/s", "cores": threads, "kind": "port",
+    return {"value": round(S / total, 2), "unit": "tok/s", "cores": threads, "cpu_model": cpu_model(), "kind": "port",
             "sample": "oracle fp32 torch-CPU: decoder layer 0 (%.2f s) + lm_head over %d rows (%.2f s) "
                       "at seq %d, scaled to %d layers" % (t_layer, S, t_lm, S, m.L),
             "ms_per_prefill_est": round(total * 1e3, 1)}
@@ -167,6 +179,8 @@ def main():
     ap.add_argument("--preset", default="qwen2.5-7b")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-dag", action="store_true", help="skip the mm -> consumer DAG workloads")
+    ap.add_argument("--no-ablation", action="store_true",
+                    help="skip the fusion-only and flag-relay-only programs")
     ap.add_argument("--keep", default=None, help="keep / reuse the model directory here")
     ap.add_argument("--profile-gemm", nargs=3, type=int, metavar=("M", "N", "K"),
                     help="only launch the producer GEMM --reps times (for rocprofv3 --pmc)")
@@ -211,17 +225,38 @@ def main():
             log("model dir written in %.1f s" % (time.time() - t0))
         runs = {}
         os.environ["KR_TIME_GATE_UP"] = "1"
-        for mode in ("graph_whole", "relay_split:%d" % args.tiles):
-            log("kr_qwen_run %s (warmup %d, steps %d)" % (mode, args.warmup, args.steps))
-            r = libapi.qwen_run(tmp, mode=mode, seq=S, device=0, warmup=args.warmup, iters=args.steps)
+        split_mode = "relay_split:%d" % args.tiles
+        # serial; the relay split as shipped (o and down release k row tiles
+        # to Add+RMSNorm through device flags, SwiGLU in the gate/up
+        # epilogue); and two ablations separating the flag relays from the
+        # epilogue fusion
+        plan = [("serial", "graph_whole", {}), ("split", split_mode, {})]
+        if not args.no_ablation:
+            plan += [("fusion_only", split_mode, {"KR_SPLIT_NORM": "0"}),
+                     ("flag_relay_only", split_mode, {"KR_SPLIT_SWIGLU": "kernel"})]
+        for name, mode, env in plan:
+            log("kr_qwen_run %s %s %s (warmup %d, steps %d)" % (name, mode, env or "", args.warmup, args.steps))
+            saved = {k: os.environ.get(k) for k in env}
+            os.environ.update(env)
+            try:
+                r = libapi.qwen_run(tmp, mode=mode, seq=S, device=0, warmup=args.warmup, iters=args.steps)
+            finally:
+                for k, v in saved.items():
+                    if v is None:
+                        os.environ.pop(k, None)
+                    else:
+                        os.environ[k] = v
             if r.get("_rc") != 0:
-                raise RuntimeError("%s failed: %s" % (mode, r.get("error")))
-            log("  best %.1f us typical %.1f us argmax %s timeouts %s" % (
-                r["best_us"], r["typical_us"], r["argmax"], r["flag_timeouts"]))
-            runs[mode] = r
-        serial, split = runs["graph_whole"], runs["relay_split:%d" % args.tiles]
-        if serial["logits_fnv64"] != split["logits_fnv64"]:
-            raise RuntimeError("relay split logits differ from serial")
+                raise RuntimeError("%s failed: %s" % (name, r.get("error")))
+            log("  best %.1f us typical %.1f us argmax %s flag edges %s timeouts %s" % (
+                r["best_us"], r["typical_us"], r["argmax"], r["flag_edges"], r["flag_timeouts"]))
+            if r["flag_timeouts"] != 0:
+                raise RuntimeError("%s: %d flag waits timed out" % (name, r["flag_timeouts"]))
+            runs[name] = r
+        serial, split = runs["serial"], runs["split"]
+        for name, r in runs.items():
+            if r["logits_fnv64"] != serial["logits_fnv64"]:
+                raise RuntimeError("%s logits differ from serial" % name)
         I, H = cfg["intermediate_size"], cfg["hidden_size"]
         roof = gemm_roofline(split, serial, S, 2 * I, H)
         total_split_s = sum(split["samples_us"]) / 1e6
@@ -237,6 +272,21 @@ def main():
         if not args.no_cpu:
             log("cpu baseline (oracle, bounded sample)")
             cpu = cpu_baseline(tmp)
+        relay = split["flag_edges"] > 0
+        if relay:
+            workload = ("%s-shaped prefill, batch 1, seq %d: relay split, o and down projections each releasing %d "
+                        "row tiles to their Add+RMSNorm through device flags (%d flag edges per prefill), SwiGLU "
+                        "fused into the gate/up GEMM epilogue" % (PRESET_NAMES.get(args.preset, args.preset), S,
+                                                                   args.tiles, split["flag_edges"]))
+        else:
+            workload = ("%s-shaped prefill, batch 1, seq %d: serial program with SwiGLU fused into the gate/up "
+                        "GEMM epilogue (no flag relay at this shape)" % (PRESET_NAMES.get(args.preset, args.preset), S))
+
+        def ms(r):
+            return round(sum(r["samples_us"]) / len(r["samples_us"]) / 1e3, 3)
+
+        breakdown = {name: {"ms_per_step": ms(r), "vs_serial": round(ms(serial) / ms(r), 4),
+                            "flag_edges": r["flag_edges"]} for name, r in runs.items()}
         out = {
             "metric": "Qwen2.5-7B prefill tok/s @seq2048 1 GPU; split-vs-serial speedup; MFMA util",
             "value": round(value, 1), "unit": "tok/s", "n_gpus": 1, "steps": args.steps,
@@ -246,13 +296,15 @@ def main():
             "vs_baseline": round(value / REF_BEST_TOK_S, 3) if (args.preset, S) == ("qwen2.5-7b", 2048) else None,
             "dtype": "bf16",
             "data": "synthetic (random-init N(0,0.02) bf16 weights, uniform token ids)",
-            "config": {"workload": "%s-shaped prefill, batch 1, seq %d, relay split %d tiles"
-                       % (PRESET_NAMES.get(args.preset, args.preset), S, args.tiles), "model": args.preset,
-                       "global_batch": 1, "seq_len": S,
-                       "parallelism": "none (1 GPU)", "tiles": args.tiles},
+            "config": {"workload": workload, "model": args.preset, "global_batch": 1, "seq_len": S,
+                       "parallelism": "none (1 GPU)", "relay_tiles": args.tiles if relay else None},
             "serial_ms_per_step": round(total_serial_s * 1e3 / args.steps, 3),
             "serial_tok_s": round(args.steps * S / total_serial_s, 1),
             "split_vs_serial": round(total_serial_s / total_split_s, 4),
+            # makespan per program, each against serial: the flag relays alone
+            # (SwiGLU as the serial kernel), the epilogue fusion alone (o and
+            # down in stream order), and both (the split as shipped)
+            "relay_breakdown": breakdown,
             "best_ms": {"serial": round(serial["best_us"] / 1e3, 3), "split": round(split["best_us"] / 1e3, 3)},
             "prefill_tflops": round(flops / 1e12, 3),
             "prefill_mfma_frac": round(flops / (total_split_s / args.steps) / 1e12 / PEAK_BF16_TFLOPS, 4),

@@ -112,6 +112,26 @@ int kr_op_gemm_swiglu(int dtype, const void *A, int64_t lda, const void *Bt, int
 int kr_op_gemm_swiglu_epilogue(int dtype, const void *A, int64_t lda, const void *Bt, int64_t ldb, void *act,
                                int64_t ld_act, int M, int cols, int K, void *stream);
 
+/* Row-tiled relay of a projection to its Add+RMSNorm consumer (the
+ * reference's down -> Add+RMSNorm tile loop, exec/qwen_main.cpp:1274-1302,
+ * on one device and without the all-reduce; the consumer is aclnnAddRmsNorm,
+ * :548-565): C[M,N] = A . Bt^T is released in relay tiles of
+ * pub->rows_per_tile rows through pub's control blocks, and as soon as a
+ * tile is released the launch's own workgroups compute, for each of its rows,
+ * sum = bf16(res + C) and y = bf16(gamma * bf16(sum * rstd)),
+ * rstd = 1/sqrt(mean(sum^2) + eps) (rstd_out fp32 [M], optional; sum may be
+ * NULL), bit-identical to kr_op_rowop(KR_ROW_ADD_RMSNORM) over C. Each
+ * release is consumed by the same launch: the tile's block ends with
+ * consumed advanced and status 1 (2 if a wait ran past max_spins). C, res,
+ * y and sum are packed [M, N]; N in 136..4096, a multiple of 8. ws/counters
+ * as for kr_op_gemm_streamk (NULL: data-parallel tiles). Fails (non-zero)
+ * when a relay tile's producer workgroups cannot all be resident at once:
+ * use smaller relay tiles. */
+int kr_op_gemm_add_rmsnorm(int dtype, const void *A, int64_t lda, const void *Bt, int64_t ldb, void *C, int M,
+                           int N, int K, const void *res, const void *gamma, void *y, void *sum, float *rstd_out,
+                           float eps, const kr_pub *pub, uint32_t max_spins, void *ws, size_t ws_bytes,
+                           int32_t *counters, int n_counters, void *stream);
+
 /* Stream-K GEMM for shapes whose 256x256 output tiles are fewer than the CUs
  * (the reference's q/k/v, o and down projections at prefill sizes,
  * exec/qwen_main.cpp:499-512, 1336-1344): every CU takes an equal run of the

@@ -59,6 +59,23 @@ struct GemmDesc {
     int order_rows = 0;          // > 0: produce in runs of this many rows (a
                                  // multiple of pub.rows_per_tile), default
                                  // one run per relay tile
+    // Add+RMSNorm relay consumer (requires pub; C packed, ldc == N; N a
+    // one-wave row, 136..4096 columns): once a relay tile is released, the
+    // producer's own workgroups compute, for each of its rows,
+    //   norm_sum = res + C,  norm_y = rmsnorm(norm_sum) * gamma
+    // ([M, N] packed; norm_rstd fp32 [M] optional) with the standalone
+    // Add+RMSNorm kernel's row code (same bits). The edge's control blocks
+    // are pub's: each relay tile's release is consumed by this launch
+    // (consumed + 1, status 1 = ok, 2 = a wait exceeded norm_max_spins).
+    // Only where every relay tile's producer workgroups fit the device at
+    // once (GemmLaunch throws otherwise).
+    const void *norm_res = nullptr;
+    const void *norm_gamma = nullptr;
+    void *norm_y = nullptr;
+    void *norm_sum = nullptr;
+    float *norm_rstd = nullptr;
+    float norm_eps = 1e-6f;
+    uint32_t norm_max_spins = kDefaultMaxSpins;
 };
 
 // Launch C = A . Bt^T (+bias). pub.rows_per_tile (when publishing) must be a
@@ -69,6 +86,11 @@ struct GemmDesc {
 // every workgroup first waits for the producer tiles covering its rows of A,
 // and the launch consumes wait.adv_lo..adv_hi once all workgroups are done.
 void GemmLaunch(const GemmDesc &d, hipStream_t stream);
+
+// True when GemmLaunch can run the Add+RMSNorm relay consumer for this shape
+// and relay tile (rows_per_tile): a one-wave row width, whole tiles, and the
+// producer workgroups of one relay tile resident at once.
+bool GemmNormRelayFits(int M, int N, int K, int rows_per_tile, bool streamk_ws);
 
 // Workspace a stream-K launch of this shape needs (0 bytes, 0 counters: the
 // launch runs data-parallel).

@@ -25,6 +25,7 @@
 //   releases the tile.
 #include "kr_gemm.h"
 #include "kr_relay.h"
+#include "kr_rowcore.h"
 
 namespace kr {
 
@@ -64,6 +65,17 @@ struct GemmParams {
     const uint16_t *rope_cos;  // RoPE epilogue (nullptr: none)
     const uint16_t *rope_sin;
     int rope_cols, rope_d, rope_pos0;
+    // Add+RMSNorm relay consumer run by the producer's workgroups (rn_y ==
+    // nullptr: none): y = rmsnorm(res + C) * gamma, sum = res + C, per row of
+    // every released relay tile; all [M, N] packed
+    const uint16_t *rn_res;
+    const uint16_t *rn_gamma;
+    uint16_t *rn_y;
+    uint16_t *rn_sum;
+    float *rn_rstd;
+    float rn_eps;
+    int rn_cpl;          // chunks per lane of a one-wave row (1, 2, 4, 8)
+    uint32_t rn_spins;   // spin bound of the wait on a relay tile
 };
 
 __device__ __forceinline__ int Swz(int row, int chunk) { return chunk ^ ((row >> 1) & 7); }
@@ -195,6 +207,60 @@ __device__ void TailSwiglu(const GemmParams &p)
     if (threadIdx.x == 0) {
         const int32_t a = __hip_atomic_fetch_add(flag + kOffDone, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         if (a == p.tail_wpt - 1) {
+            StoreRelaxed(flag + kOffDone, 0);
+            const int32_t to = __hip_atomic_exchange(flag + kOffTimedOut, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            StoreRelaxed(flag + kOffConsumed, LoadRelaxed(flag + kOffConsumed) + 1);
+            StoreRelaxed(flag + kOffStatus, to ? 2 : 1);
+        }
+    }
+}
+
+// ------------------------------------------- Add+RMSNorm relay consumer
+// The producer's own workgroups consume its released row tiles (the
+// reference's down -> Add+RMSNorm tile loop, exec/qwen_main.cpp:1274-1302,
+// without the all-reduce): a workgroup that has stored its C tile and arrived
+// on relay tile `tile`'s flag waits for the tile's release (all of its
+// producer workgroups have arrived), then computes Add+RMSNorm for rows
+// lo + worker*waves + wave, stepping by workers*waves, one row per wave at a
+// time, with the row code of the standalone row kernel. C is read at device
+// scope (written by other XCDs' workgroups of this launch). The last of the
+// tile's `workers` consumes the release (consumed + 1, status 1, or 2 when
+// any wait ran out of spins). Safe from deadlock because the launcher only
+// asks for it when a relay tile's producer workgroups fit the device at once
+// (they are dispatched in order, so they are all resident or finished).
+template <int DT, int CPL>
+__device__ __forceinline__ void NormRows(const GemmParams &p, int lo, int hi, int first, int step)
+{
+    const int ln = threadIdx.x & 63;
+    for (int r = lo + first; r < hi; r += step) {
+        const int64_t o = int64_t(r) * p.N;
+        AddRmsNormRow<DT, CPL, true>(p.rn_res + o, p.C + o, p.rn_gamma, p.rn_y + o,
+                                     p.rn_sum != nullptr ? p.rn_sum + o : nullptr,
+                                     p.rn_rstd != nullptr ? p.rn_rstd + r : nullptr, p.N, p.rn_eps, ln, false);
+    }
+}
+
+template <int DT>
+__device__ void NormTail(const GemmParams &p, int tile, int worker, int workers)
+{
+    int32_t *flag = p.pub.ctrl + size_t(p.pub.flag0 + tile) * kWords;
+    if (threadIdx.x == 0) SpinOnTile(flag, flag, p.rn_spins);
+    __syncthreads();
+    const int R = p.pub.rows_per_tile;
+    const int lo = tile * R, hi = min(lo + R, p.M);
+    const int nw = int(blockDim.x) >> 6;
+    const int first = worker * nw + int(threadIdx.x >> 6);
+    const int step = workers * nw;
+    switch (p.rn_cpl) {
+        case 1: NormRows<DT, 1>(p, lo, hi, first, step); break;
+        case 2: NormRows<DT, 2>(p, lo, hi, first, step); break;
+        case 4: NormRows<DT, 4>(p, lo, hi, first, step); break;
+        default: NormRows<DT, 8>(p, lo, hi, first, step); break;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const int32_t a = __hip_atomic_fetch_add(flag + kOffDone, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (a == workers - 1) {
             StoreRelaxed(flag + kOffDone, 0);
             const int32_t to = __hip_atomic_exchange(flag + kOffTimedOut, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             StoreRelaxed(flag + kOffConsumed, LoadRelaxed(flag + kOffConsumed) + 1);
@@ -490,7 +556,11 @@ GemmKernel(GemmParams p)
     } else {
         StoreTile<DT, BM, BN, kThreads>(p, acc, smem, m0, n0, wm, wn, lane);
     }
-    if (p.pub.ctrl != nullptr) RelayArrive(p.pub, m0 / p.pub.rows_per_tile);
+    if (p.pub.ctrl != nullptr) {
+        RelayArrive(p.pub, m0 / p.pub.rows_per_tile);
+        // relay order: workgroups [t*arrivals, (t+1)*arrivals) make tile t
+        if (p.rn_y != nullptr) NormTail<DT>(p, m0 / p.pub.rows_per_tile, int(blockIdx.x) % p.pub.arrivals, p.pub.arrivals);
+    }
     RelayFinish(p.wait);
 }
 
@@ -621,6 +691,21 @@ int CuCount()
     return v;
 }
 
+// The Add+RMSNorm relay consumer waits inside the producer's workgroups for
+// the other producer workgroups of its relay tile. Workgroups are dispatched
+// in id order (per XCD) and a relay tile's are consecutive ids, so the waits
+// always end when a relay tile's workgroups fit the device at once: then
+// every earlier tile's workgroups are resident or finished. A stream-K grid
+// is resident as a whole (one workgroup per CU).
+bool NormRelayResident(int bm, int bn, int M, int N, int rows_per_tile, int sk_wgs)
+{
+    if (sk_wgs > 0) return sk_wgs <= CuCount();
+    if (rows_per_tile <= 0 || rows_per_tile % bm != 0 || M % rows_per_tile != 0) return false;
+    const int per = (rows_per_tile / bm) * ((N + bn - 1) / bn);
+    const int slots = CuCount() * (bm * bn >= 256 * 128 ? 1 : 2);
+    return per <= slots;
+}
+
 // Stream-K plan of a GEMM whose data-parallel tiling leaves CUs idle.
 // Default: an exact split of K over 256x256 tiles, S = CUs / tiles pieces per
 // tile, each piece at least 16 K stages (S >= 2), so every workgroup runs one
@@ -695,6 +780,13 @@ void LaunchTyped(const GemmParams &base, int order_rows, int tail_tiles, hipStre
     }
     p.gemm_wgs = p.tiles_m * p.tiles_n;
     p.group_m = RasterGroupM();
+    if (p.rn_y != nullptr) {
+        if (sk == nullptr && p.order_rows != p.pub.rows_per_tile)
+            throw std::runtime_error("gemm: the Add+RMSNorm relay consumer needs the default relay-tile order");
+        if (!NormRelayResident(BM, BN, p.M, p.N, p.pub.rows_per_tile, sk != nullptr ? sk->G : 0))
+            throw std::runtime_error("gemm: a relay tile's producer workgroups do not fit the device at once; "
+                                     "the Add+RMSNorm relay consumer would wait on workgroups not yet placed");
+    }
     if (sk != nullptr) {
         if (BM != 256 || BN != 256 || sk->tiles != p.gemm_wgs) throw std::logic_error("gemm: stream-K plan mismatch");
         p.sk_wgs = sk->G;
@@ -798,6 +890,21 @@ GemmTile GemmPickTile(int M, int N, int relay_rows, bool coresident)
     return best.bm < 0 ? best : pick192(best);
 }
 
+bool GemmNormRelayFits(int M, int N, int K, int rows_per_tile, bool streamk_ws)
+{
+    if (AddRmsNormRowCpl(N) == 0 || rows_per_tile <= 0 || M % rows_per_tile != 0) return false;
+    StreamKPlan skp;
+    const bool sk_pub_ok = rows_per_tile % 256 == 0 || 256 % rows_per_tile == 0;
+    if (streamk_ws && sk_pub_ok && !ForceSimple() && PlanStreamK(M, N, K, skp)) return skp.G <= CuCount();
+    GemmTile t = GemmPickTile(M, N, rows_per_tile, false);
+    if (const char *e = std::getenv("KR_GEMM_TILE")) {
+        int bm = 0, bn = 0;
+        if (std::sscanf(e, "%dx%d", &bm, &bn) == 2 && rows_per_tile % bm == 0) t = {bm, bn};
+    }
+    if (t.bm <= 0 || t.bm == 192) t = {256, 256};
+    return NormRelayResident(t.bm, t.bn, M, N, rows_per_tile, 0);
+}
+
 void GemmStreamKNeeds(int M, int N, int K, size_t *ws_bytes, int *counters)
 {
     StreamKPlan pl;
@@ -865,6 +972,28 @@ void GemmLaunch(const GemmDesc &d, hipStream_t stream)
         if ((reinterpret_cast<uintptr_t>(d.C) | reinterpret_cast<uintptr_t>(d.tail_act)) & 15)
             throw std::runtime_error("gemm tail: buffers must be 16-byte aligned");
     }
+    if (d.norm_y != nullptr) {
+        if (d.pub.ctrl == nullptr || d.pub.rows_per_tile <= 0 || d.M % d.pub.rows_per_tile != 0)
+            throw std::runtime_error("gemm add_rmsnorm: needs a relay release over whole tiles of M");
+        if (d.norm_res == nullptr || d.norm_gamma == nullptr)
+            throw std::runtime_error("gemm add_rmsnorm: residual and gamma are required");
+        if (p.epi_act != nullptr || p.tail_act != nullptr || d.rope_cos != nullptr || d.order_rows != 0)
+            throw std::runtime_error("gemm add_rmsnorm: excludes the SwiGLU epilogue/tail, RoPE and order_rows");
+        if (d.ldc != d.N || AddRmsNormRowCpl(d.N) == 0)
+            throw std::runtime_error("gemm add_rmsnorm: C must be packed (ldc == N) with N in 136..4096, N % 8 == 0");
+        if ((reinterpret_cast<uintptr_t>(d.C) | reinterpret_cast<uintptr_t>(d.norm_res) |
+             reinterpret_cast<uintptr_t>(d.norm_gamma) | reinterpret_cast<uintptr_t>(d.norm_y) |
+             reinterpret_cast<uintptr_t>(d.norm_sum)) & 15)
+            throw std::runtime_error("gemm add_rmsnorm: buffers must be 16-byte aligned");
+        p.rn_res = static_cast<const uint16_t *>(d.norm_res);
+        p.rn_gamma = static_cast<const uint16_t *>(d.norm_gamma);
+        p.rn_y = static_cast<uint16_t *>(d.norm_y);
+        p.rn_sum = static_cast<uint16_t *>(d.norm_sum);
+        p.rn_rstd = d.norm_rstd;
+        p.rn_eps = d.norm_eps;
+        p.rn_cpl = AddRmsNormRowCpl(d.N);
+        p.rn_spins = d.norm_max_spins > 0 ? d.norm_max_spins : kDefaultMaxSpins;
+    }
     if (p.wait.ctrl != nullptr && p.wait.prod_rows <= 0) throw std::runtime_error("gemm: wait.prod_rows must be > 0");
     const int relay_rows = d.pub.ctrl != nullptr ? d.pub.rows_per_tile : 0;
     GemmTile t = GemmPickTile(d.M, d.N, relay_rows, d.coresident);
@@ -903,7 +1032,8 @@ void GemmLaunch(const GemmDesc &d, hipStream_t stream)
         d.pub.ctrl == nullptr || (rpt > 0 && (rpt % 256 == 0 || 256 % rpt == 0) && d.M % rpt == 0);
     if (d.streamk && sk_pub_ok && d.wait.ctrl == nullptr && d.tail_act == nullptr && d.epi_act == nullptr && !ForceSimple() &&
         d.bm == 0 && d.bn == 0 && PlanStreamK(d.M, d.N, d.K, skp) && d.sk_ws != nullptr && d.sk_cnt != nullptr &&
-        d.sk_ws_bytes >= size_t(skp.tiles) * skp.pmax * 256 * 256 * 4 && d.sk_cnt_len >= skp.tiles) {
+        d.sk_ws_bytes >= size_t(skp.tiles) * skp.pmax * 256 * 256 * 4 && d.sk_cnt_len >= skp.tiles &&
+        (d.norm_y == nullptr || skp.G <= CuCount())) {
         p.sk_ws = static_cast<float *>(d.sk_ws);
         p.sk_cnt = d.sk_cnt;
         bf ? LaunchTyped<kBF16, 256, 256>(p, 0, 0, stream, &skp) : LaunchTyped<kF16, 256, 256>(p, 0, 0, stream, &skp);

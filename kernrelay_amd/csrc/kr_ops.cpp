@@ -116,6 +116,43 @@ int kr_op_gemm_swiglu(int dtype, const void *A, int64_t lda, const void *Bt, int
     });
 }
 
+int kr_op_gemm_add_rmsnorm(int dtype, const void *A, int64_t lda, const void *Bt, int64_t ldb, void *C, int M,
+                           int N, int K, const void *res, const void *gamma, void *y, void *sum, float *rstd_out,
+                           float eps, const kr_pub *pub, uint32_t max_spins, void *ws, size_t ws_bytes,
+                           int32_t *counters, int n_counters, void *stream)
+{
+    return Guard([&] {
+        if (pub == nullptr || pub->ctrl == nullptr) throw std::runtime_error("gemm add_rmsnorm: needs a relay release");
+        kr::GemmDesc d;
+        d.dtype = dtype;
+        d.A = A;
+        d.Bt = Bt;
+        d.C = C;
+        d.lda = lda;
+        d.ldb = ldb;
+        d.ldc = N;
+        d.M = M;
+        d.N = N;
+        d.K = K;
+        d.pub = ToPub(pub);
+        d.norm_res = res;
+        d.norm_gamma = gamma;
+        d.norm_y = y;
+        d.norm_sum = sum;
+        d.norm_rstd = rstd_out;
+        d.norm_eps = eps;
+        d.norm_max_spins = max_spins;
+        if (ws != nullptr) {
+            d.streamk = true;
+            d.sk_ws = ws;
+            d.sk_ws_bytes = ws_bytes;
+            d.sk_cnt = counters;
+            d.sk_cnt_len = n_counters;
+        }
+        kr::GemmLaunch(d, S(stream));
+    });
+}
+
 int kr_op_gemm_streamk_workspace(int M, int N, int K, size_t *ws_bytes, int *counters)
 {
     return Guard([&] {

@@ -25,12 +25,16 @@
 //   serial_fused / graph_whole one stream, fused Add+RMSNorm
 //   relay_event                two streams, whole ops, hipEvent edges
 //   relay_flag(_graph)         two streams, whole ops, device-flag edges
-//   relay_split[:k]            two streams, device flags, the o, gate/up and
-//                              down producers release k row tiles from their
-//                              epilogues and the Add+RMSNorm / SwiGLU
-//                              consumers start per tile (per-stream graphs)
-// The producer stream runs GEMMs, RoPE and attention; the consumer stream runs
-// Add+RMSNorm and SwiGLU (the reference's AIC/AIV split, BuildDual :811-923).
+//   relay_split[:k]            one stream, one graph: the o and down GEMMs
+//                              release k row tiles through device flags and
+//                              each released tile's Add+RMSNorm runs in the
+//                              GEMM's own workgroups (the reference's per-tile
+//                              down -> AddRmsNorm loop, BuildTP :1274-1302,
+//                              without the all-reduce); SwiGLU is fused into
+//                              the gate/up GEMM's epilogue
+// In the two-stream modes the producer stream runs GEMMs, RoPE and attention
+// and the consumer stream Add+RMSNorm and SwiGLU (the reference's AIC/AIV
+// split, BuildDual :811-923).
 #include <fcntl.h>
 #include <sys/mman.h>
 #include <sys/stat.h>
@@ -823,12 +827,30 @@ private:
         // SwiGLU: in the gate/up GEMM's epilogue (default), or a consumer
         // appended to its launch waiting on its k released row tiles
         // (KR_SPLIT_SWIGLU=flags)
-        const bool swiglu_epi = EnvStr("KR_SPLIT_SWIGLU", "epilogue") != "flags";
-        const int gu_act = swiglu_epi ? 0 : NewEdge(k * L_);  // block (l, t) = gu_act + l*k + t
+        // (KR_SPLIT_SWIGLU=kernel: the serial schedule's GEMM then SwiGLU
+        // kernel, to measure the flag relays without the fusion)
+        const std::string swiglu_mode = EnvStr("KR_SPLIT_SWIGLU", "epilogue");
+        if (swiglu_mode != "epilogue" && swiglu_mode != "flags" && swiglu_mode != "kernel")
+            throw std::runtime_error("KR_SPLIT_SWIGLU must be epilogue, flags or kernel");
+        const bool swiglu_epi = swiglu_mode == "epilogue";
+        const bool swiglu_kernel = swiglu_mode == "kernel";
+        const int gu_act = swiglu_mode == "flags" ? NewEdge(k * L_) : 0;  // block (l, t) = gu_act + l*k + t
         const int order_rows = EnvInt("KR_SPLIT_ORDER_ROWS", k >= 4 ? S / 2 : T);
         const int tail_tiles = std::max(0, std::min(k, EnvInt("KR_SPLIT_TAIL_TILES", k >= 4 ? k / 2 : k - 1)));
         if (order_rows <= 0 || order_rows % T != 0 || S % order_rows != 0)
             throw std::runtime_error("relay_split: KR_SPLIT_ORDER_ROWS must be a multiple of seq/tiles dividing seq");
+        // o -> Add+RMSNorm and down -> Add+RMSNorm: the GEMM releases its k
+        // row tiles, and each released tile's Add+RMSNorm runs at once in the
+        // producer's own workgroups (block (l, t) = edge + l*k + t), where a
+        // relay tile's producer workgroups fit the device at once
+        // (KR_SPLIT_NORM=0: Add+RMSNorm as a kernel after the GEMM)
+        const bool norm_env = EnvInt("KR_SPLIT_NORM", 1) != 0;
+        const bool o_relay = norm_env && GemmNormRelayFits(S, H_, HQ_ * D_, T, skws_bytes_ > 0);
+        const bool d_relay = norm_env && GemmNormRelayFits(S, H_, I_, T, skws_bytes_ > 0);
+        const int o_edge = o_relay ? NewEdge(k * L_) : 0;
+        const int d_edge = d_relay ? NewEdge(k * L_) : 0;
+        for (int b = 0; b < (o_relay ? k * L_ : 0); ++b) consumed_.push_back(o_edge + b);
+        for (int b = 0; b < (d_relay ? k * L_ : 0); ++b) consumed_.push_back(d_edge + b);
         ctrl_.Alloc(std::max<size_t>(ctrl_blocks_, 1) * kWords * 4);
         Check(hipMemset(ctrl_.get(), 0, ctrl_.bytes()), "zero ctrl");
         max_spins_ = uint32_t(EnvInt("KR_MAX_SPINS", int(kDefaultMaxSpins)));
@@ -847,9 +869,26 @@ private:
         for (int l = 0; l < L_; ++l) {
             const Layer &w = layers_[l];
             EmitAttention(P, l, RelayWait{});
-            Gemm(P, attn_.get(), int64_t(HQ_) * D_, w.o, H_, HQ_ * D_, o_.get(), H_, nullptr, S, RelayPub{});
-            AddRmsNorm(P, hcur, o_.get(), w.ln2, x, hnxt, RelayWait{}, 0, RelayPub{}, 0);
-            if (swiglu_epi) {
+            if (o_relay) {
+                GemmNormRelay(P, attn_.get(), int64_t(HQ_) * D_, w.o, HQ_ * D_, o_.get(), Pub(o_edge + l * k, T), hcur,
+                              w.ln2, x, hnxt);
+            } else {
+                Gemm(P, attn_.get(), int64_t(HQ_) * D_, w.o, H_, HQ_ * D_, o_.get(), H_, nullptr, S, RelayPub{});
+                AddRmsNorm(P, hcur, o_.get(), w.ln2, x, hnxt, RelayWait{}, 0, RelayPub{}, 0);
+            }
+            if (swiglu_kernel) {
+                Timed(P, [&] {
+                    Gemm(P, x, H_, w.gu, 2 * I_, H_, gu_.get(), 2 * int64_t(I_), nullptr, S, RelayPub{}, RelayWait{},
+                         false);
+                });
+                EwDesc e;
+                e.op = kEwSwigluGU;
+                e.x0 = gu_.get();
+                e.y = act_.get();
+                e.rows = S;
+                e.cols = I_;
+                Emit(P, [e](hipStream_t st) { EwLaunch(e, st); });
+            } else if (swiglu_epi) {
                 // gate/up with SwiGLU in its epilogue: each MFMA tile hands
                 // its gate/up pairs to the consumer in registers and only act
                 // is written
@@ -903,12 +942,36 @@ private:
                     Emit(P, [e](hipStream_t st) { EwLaunch(e, st); });
                 }
             }
-            Gemm(P, act_.get(), I_, w.down, H_, I_, down_.get(), H_, nullptr, S, RelayPub{});
             const bool last = l + 1 == L_;
-            AddRmsNorm(P, hnxt, down_.get(), last ? final_norm_ : layers_[l + 1].ln1, last ? xf_.get() : x_.get(),
-                       last ? hf_.get() : static_cast<void *>(hcur), RelayWait{}, 0, RelayPub{}, 0);
+            const uint16_t *g_next = last ? final_norm_ : layers_[l + 1].ln1;
+            void *y_next = last ? xf_.get() : x_.get();
+            void *h_next = last ? hf_.get() : static_cast<void *>(hcur);
+            if (d_relay) {
+                GemmNormRelay(P, act_.get(), I_, w.down, I_, down_.get(), Pub(d_edge + l * k, T), hnxt, g_next, y_next,
+                              h_next);
+            } else {
+                Gemm(P, act_.get(), I_, w.down, H_, I_, down_.get(), H_, nullptr, S, RelayPub{});
+                AddRmsNorm(P, hnxt, down_.get(), g_next, y_next, h_next, RelayWait{}, 0, RelayPub{}, 0);
+            }
         }
         Gemm(P, xf_.get(), H_, lm_, V_, H_, logits_.get(), V_, nullptr, S, RelayPub{});
+    }
+
+    // A [S, H] projection (o or down) into C whose k released row tiles are
+    // consumed by Add+RMSNorm(res + C) in the GEMM's own workgroups: y = the
+    // next GEMM's normed input, sum = the next residual.
+    void GemmNormRelay(int s, const void *A, int64_t lda, const uint16_t *Bt, int K, void *C, RelayPub pub,
+                       const void *res, const uint16_t *gamma, void *y, void *sum)
+    {
+        GemmDesc d = MakeGemm(A, lda, Bt, H_, K, C, H_, nullptr, seq_, pub, RelayWait{});
+        d.norm_res = res;
+        d.norm_gamma = gamma;
+        d.norm_y = y;
+        d.norm_sum = sum;
+        d.norm_rstd = rstd_.as<float>();
+        d.norm_eps = float(eps_);
+        d.norm_max_spins = max_spins_;
+        Emit(s, [d](hipStream_t st) { GemmLaunch(d, st); });
     }
 
     void BuildProgram()

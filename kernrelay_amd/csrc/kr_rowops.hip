@@ -18,6 +18,7 @@
 // tree (per-lane serial, then xor-butterfly, then waves in index order) that
 // depends only on `cols`, never on the tiling, so split == unsplit bit-exact.
 #include "kr_rowops.h"
+#include "kr_rowcore.h"
 
 #include <algorithm>
 
@@ -167,6 +168,16 @@ __global__ void __launch_bounds__(kThreads) RowKernel(RowParams p)
             const int rr = active ? r : r_lo;
             const int64_t base = int64_t(rr) * p.cols;
             const int64_t ibase = int64_t(rr / p.in_group) * p.in_ld + int64_t(rr % p.in_group) * p.cols;
+            if constexpr (OP == kRowAddRmsNorm && LPR == 64) {
+                // one row per wave: the row code the producer GEMM's relay
+                // consumer runs too (kr_rowcore.h), so both give the same bits
+                if (active)
+                    AddRmsNormRow<DT, CPL, false>(p.x0 + ibase, p.x1 + ibase, p.gamma, p.y + base,
+                                                  p.sum_out != nullptr ? p.sum_out + base : nullptr,
+                                                  p.rstd_out != nullptr ? p.rstd_out + r : nullptr, p.cols, p.eps, ln,
+                                                  coh);
+                continue;
+            }
             float v[CPL][8];
             bool ok[CPL];
 #pragma unroll

@@ -80,14 +80,17 @@ class _Writer:
 
 
 def write_model_dir(out_dir, preset_or_config, seq=2048, seed=1234, max_pos=None, layers=None,
-                    device=None, std=0.02):
+                    device=None, std=0.02, gain_std=None):
     """Write a random-init model directory; returns its Path.
 
     preset_or_config: a PRESETS key or a config dict with the same keys.
     layers: override num_hidden_layers (short stacks for tests).
     device: torch device for weight generation ("cuda" generates on the GPU,
     which is much faster for the 7B/8B presets); values are the file's.
+    gain_std: spread of the RMSNorm gains around 1 (default: std); a wide
+    spread makes a misplaced or dropped gain stand out in a comparison.
     """
+    gain_std = std if gain_std is None else gain_std
     cfg = dict(PRESETS[preset_or_config]) if isinstance(preset_or_config, str) else dict(preset_or_config)
     if layers is not None:
         cfg["num_hidden_layers"] = int(layers)
@@ -100,8 +103,9 @@ def write_model_dir(out_dir, preset_or_config, seq=2048, seed=1234, max_pos=None
     dev = torch.device(device or "cpu")
     gen = torch.Generator(device=dev).manual_seed(seed)
 
-    def normal(*shape, mean=0.0):
-        t = torch.empty(*shape, dtype=torch.float32, device=dev).normal_(mean, std, generator=gen)
+    def normal(*shape, mean=0.0, sd=None):
+        t = torch.empty(*shape, dtype=torch.float32, device=dev).normal_(mean, std if sd is None else sd,
+                                                                          generator=gen)
         return t.to(torch.bfloat16).cpu()
 
     w = _Writer(out / "weights.bin")
@@ -116,15 +120,15 @@ def write_model_dir(out_dir, preset_or_config, seq=2048, seed=1234, max_pos=None
         for role, (k, n) in (("gate_proj", (H, I)), ("up_proj", (H, I)), ("down_proj", (I, H))):
             w.put(p + role + ".weight_t", normal(k, n), source_shape=(n, k))
         for role in ("input_layernorm", "post_attention_layernorm"):
-            w.put(p + role + ".weight", normal(H, mean=1.0))
+            w.put(p + role + ".weight", normal(H, mean=1.0, sd=gain_std))
         if cfg.get("qk_norm", False):
             for role in ("q_norm", "k_norm"):
-                w.put(p + role + ".weight", normal(D, mean=1.0))
+                w.put(p + role + ".weight", normal(D, mean=1.0, sd=gain_std))
     emb = normal(V, H)
     w.put("embed.weight", emb)
     lm = emb if cfg.get("tie_word_embeddings", True) else normal(V, H)
     w.put("lm_head.weight_t", lm.t().contiguous(), source_shape=(V, H))
-    w.put("final_norm.weight", normal(H, mean=1.0))
+    w.put("final_norm.weight", normal(H, mean=1.0, sd=gain_std))
     cos, sin = rope_table(max_pos, D, cfg.get("rope_theta", 1e6))
     w.put("rope.cos", cos)
     w.put("rope.sin", sin)
@@ -143,7 +147,7 @@ def write_model_dir(out_dir, preset_or_config, seq=2048, seed=1234, max_pos=None
             "rope_theta": cfg.get("rope_theta", 1e6), "hidden_act": "silu",
         },
         "tensors": w.tensors, "seq": seq, "seed": seed, "max_pos": max_pos,
-        "init": {"kind": "normal", "std": std, "norm_gain_mean": 1.0},
+        "init": {"kind": "normal", "std": std, "norm_gain_mean": 1.0, "norm_gain_std": gain_std},
     }
     (out / "manifest.json").write_text(json.dumps(manifest, indent=1))
     return out

@@ -60,11 +60,14 @@ def _lib():
                                                     ctypes.POINTER(ctypes.c_int)]
         L.kr_op_gemm_streamk.argtypes = [i32, vp, i64, vp, i64, vp, i64, vp, i32, i32, i32, vp, ctypes.c_size_t, vp,
                                          i32, vp]
+        L.kr_op_gemm_add_rmsnorm.argtypes = [i32, vp, i64, vp, i64, vp, i32, i32, i32, vp, vp, vp, vp, vp, f32,
+                                             ctypes.POINTER(KrPub), ctypes.c_uint32, vp, ctypes.c_size_t, vp, i32, vp]
         L.kr_op_stream_create.argtypes = []
         L.kr_op_stream_create.restype = vp
         L.kr_op_stream_destroy.argtypes = [vp]
         L.kr_op_stream_destroy.restype = ctypes.c_int
         for name in ("kr_op_gemm", "kr_op_gemm_swiglu", "kr_op_gemm_swiglu_epilogue", "kr_op_gemm_streamk",
+                     "kr_op_gemm_add_rmsnorm",
                      "kr_op_gemm_streamk_workspace", "kr_op_elementwise", "kr_op_rowop", "kr_op_wait", "kr_op_publish",
                      "kr_op_embedding", "kr_op_rope", "kr_op_attention", "kr_op_attention_workspace",
                      "kr_op_attention_split", "kr_op_transpose"):
@@ -149,6 +152,22 @@ def gemm_swiglu(A, Bt, C, act, pub, tail_tiles=0, order_rows=0, stream=None):
     assert Bt.shape == (2 * cols, K) and C.shape == (M, 2 * cols) and act.shape[0] == M
     _check(_lib().kr_op_gemm_swiglu(_dt(A), _ptr(A), A.stride(0), _ptr(Bt), Bt.stride(0), _ptr(C), _ptr(act),
                                     M, cols, K, ctypes.byref(pub), tail_tiles, order_rows, _stream(stream)))
+
+
+def gemm_add_rmsnorm(A, Bt, C, res, gamma, y, pub, sum_out=None, rstd=None, eps=1e-6, ws=None, counters=None,
+                     max_spins=0, stream=None):
+    """C = A @ Bt^T released in relay tiles (pub); the launch's own
+    workgroups compute Add+RMSNorm(res + C) of each released tile (y, sum_out,
+    rstd), the bits of rowop("add_rmsnorm"). ws/counters: stream-K workspace
+    (None: data-parallel)."""
+    M, K = A.shape
+    N = Bt.shape[0]
+    assert Bt.shape[1] == K and C.shape == (M, N) and res.shape == (M, N) and y.shape == (M, N)
+    _check(_lib().kr_op_gemm_add_rmsnorm(_dt(A), _ptr(A), A.stride(0), _ptr(Bt), Bt.stride(0), _ptr(C), M, N, K,
+                                         _ptr(res), _ptr(gamma), _ptr(y), _ptr(sum_out), _ptr(rstd), ctypes.c_float(eps),
+                                         ctypes.byref(pub), ctypes.c_uint32(max_spins), _ptr(ws),
+                                         0 if ws is None else ws.numel() * ws.element_size(), _ptr(counters),
+                                         0 if counters is None else counters.numel(), _stream(stream)))
 
 
 def gemm_streamk_workspace(M, N, K):

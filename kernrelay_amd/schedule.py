@@ -2,17 +2,19 @@
 
 Behaviour follows the reference's scheduler for this path:
 
-* ``build_fixed_schedule`` — python/kernrelay/_vendor/scheduler/fixed.py:64-156:
-  every node's input rows are split evenly into its chunk count; consumer
-  tile j waits on every producer tile whose output rows intersect j's input
-  rows (the last producer tile when none do); waits are only materialised
-  across streams; tasks enter their stream in DAG topological order
-  (declaration order breaks ties);
-* ``serial_schedule`` — python/kernrelay/schedule.py:67-105: all tiles on one
-  ``aicore`` stream in a global topological order, no waits or publishes;
-* ``validate_schedule`` / ``invalid_variants`` — python/kernrelay/schedule.py:
-  108-222: the structural checks and the four deliberately broken schedules
-  whose executor error markers the E0 gate expects.
+* ``build_fixed_schedule`` — the schedule.json the reference's fixed-plan
+  writer emits (python/kernrelay/_vendor/scheduler/fixed.py:64-156): every
+  node's input rows are split evenly into its chunk count; consumer tile j
+  waits on every producer tile whose output rows meet j's input rows (the
+  last producer tile when none do); waits exist only across streams; tasks
+  enter their stream in DAG topological order (declaration order breaks
+  ties);
+* ``serial_schedule`` — the reference's serial baseline
+  (python/kernrelay/schedule.py:67-105): all tiles on one ``aicore`` stream
+  in a global topological order, no waits or publishes;
+* ``validate_schedule`` / ``invalid_variants`` — structural checks, and the
+  four deliberately broken schedules whose executor error markers the
+  reference's E0 gate expects (python/kernrelay/schedule.py:108-222).
 
 Op -> stream follows the reference's measured engine map
 (python/kernrelay/_vendor/registry/engine_map.json): matrix work on ``aic``,
@@ -159,97 +161,115 @@ def node_dims(node):
 
 
 def topo_order(dag):
-    """Kahn order; among ready nodes the earliest declared goes first."""
-    names = [n.name for n in dag.nodes]
-    pos = {n: i for i, n in enumerate(names)}
-    indeg = {n: 0 for n in names}
-    succ = {n: [] for n in names}
+    """Node names in dependency order; of the nodes whose producers are all
+    placed, the one declared first goes next (a min-heap on declaration
+    index)."""
+    import heapq
+    index = {n.name: i for i, n in enumerate(dag.nodes)}
+    waiting = {n.name: 0 for n in dag.nodes}
+    consumers = {n.name: [] for n in dag.nodes}
     for e in dag.edges:
-        indeg[e.dst] += 1
-        succ[e.src].append(e.dst)
-    ready = sorted((n for n in names if indeg[n] == 0), key=pos.get)
+        waiting[e.dst] += 1
+        consumers[e.src].append(e.dst)
+    heap = [index[name] for name, w in waiting.items() if w == 0]
+    heapq.heapify(heap)
     order = []
-    while ready:
-        cur = ready.pop(0)
-        order.append(cur)
-        for v in succ[cur]:
-            indeg[v] -= 1
-            if indeg[v] == 0:
-                ready.append(v)
-                ready.sort(key=pos.get)
-    if len(order) != len(names):
+    while heap:
+        name = dag.nodes[heapq.heappop(heap)].name
+        order.append(name)
+        for c in consumers[name]:
+            waiting[c] -= 1
+            if waiting[c] == 0:
+                heapq.heappush(heap, index[c])
+    if len(order) != len(dag.nodes):
         raise ValueError("%s: the DAG has a cycle" % dag.name)
     return order
 
 
-def build_fixed_schedule(dag, chunking=None, nranks=1, method="fixed"):
-    """DAG + fixed chunking -> schedule.json content (dict)."""
-    chunking = {k: int(v) for k, v in dict(chunking or {}).items() if int(v) > 0}
-    nm = dag.node_map
-    unknown = set(chunking) - set(nm)
-    if unknown:
-        raise ValueError("%s: chunking names unknown nodes %s" % (dag.name, sorted(unknown)))
-    for e in dag.edges:
-        if nm[e.src].op == "cast":
-            raise ValueError("%s: a cast output may only be a sink, not consumed by %s" % (dag.name, e.dst))
+@dataclass(frozen=True)
+class RowSplit:
+    """How a node's rows are cut: `chunks` tiles of `in_rows` input rows,
+    each writing `out_rows` output rows (collectives scale the output)."""
+    chunks: int
+    in_rows: int
+    out_rows: int
 
-    geom = {}
+    def tiles_covering(self, lo, hi):
+        """Tiles whose output rows meet [lo, hi). A consumer range past the
+        produced rows maps to the last tile (the conservative choice of the
+        reference's geometry, fixed.py:121-124)."""
+        first = lo // self.out_rows
+        if first >= self.chunks:
+            return [self.chunks - 1]
+        last = min((hi - 1) // self.out_rows, self.chunks - 1)
+        return list(range(first, last + 1))
+
+
+def row_splits(dag, chunking, nranks):
+    """RowSplit of every node, checking that the cuts are whole rows."""
+    out = {}
     for n in dag.nodes:
-        rows = node_rows(n)
-        chunks = chunking.get(n.name, 1)
-        if rows % chunks != 0:
-            raise ValueError("%s: node %s rows=%d not divisible by chunks=%d" % (dag.name, n.name, rows, chunks))
-        own_out = out_rows(n, nranks)
-        if own_out % chunks != 0:
-            raise ValueError("%s: node %s output rows %d not divisible by chunks=%d"
-                             % (dag.name, n.name, own_out, chunks))
-        if n.op == "reducescatter" and (rows // chunks) % nranks != 0:
+        k = chunking.get(n.name, 1)
+        rows, produced = node_rows(n), out_rows(n, nranks)
+        if rows % k:
+            raise ValueError("%s: node %s rows=%d not divisible by chunks=%d" % (dag.name, n.name, rows, k))
+        if produced % k:
+            raise ValueError("%s: node %s output rows %d not divisible by chunks=%d" % (dag.name, n.name, produced, k))
+        if n.op == "reducescatter" and (rows // k) % nranks:
             raise ValueError("%s: reducescatter %s rows per chunk must divide by nranks=%d"
                              % (dag.name, n.name, nranks))
-        geom[n.name] = (chunks, rows // chunks, own_out // chunks)
+        out[n.name] = RowSplit(k, rows // k, produced // k)
+    return out
 
-    tasks = {}
-    for n in dag.nodes:
-        chunks, per, out_per = geom[n.name]
-        for i in range(chunks):
-            tasks[(n.name, i)] = {"node": n.name, "tile": i, "wait": [], "publish": False,
-                                  "in_row_off": i * per, "in_rows": per, "out_row_off": i * out_per}
 
-    published = set()
+def _task(node, tile, split):
+    return {"node": node, "tile": tile, "wait": [], "publish": False, "in_row_off": tile * split.in_rows,
+            "in_rows": split.in_rows, "out_row_off": tile * split.out_rows}
+
+
+def build_fixed_schedule(dag, chunking=None, nranks=1, method="fixed"):
+    """DAG + per-node chunk counts -> schedule.json content (dict), the
+    format of the reference's fixed-plan writer
+    (python/kernrelay/_vendor/scheduler/fixed.py:64-156).
+
+    Each node's rows are cut into equal tiles. A consumer tile waits on every
+    producer tile whose output rows meet its input rows, but only across
+    streams (one stream's FIFO already orders its tasks), and those producer
+    tiles publish. Tasks join their op's stream in dependency order."""
+    chunking = {k: int(v) for k, v in dict(chunking or {}).items() if int(v) > 0}
+    by_name = dag.node_map
+    unknown = sorted(set(chunking) - set(by_name))
+    if unknown:
+        raise ValueError("%s: chunking names unknown nodes %s" % (dag.name, unknown))
+    sinks_only = [e for e in dag.edges if by_name[e.src].op == "cast"]
+    if sinks_only:
+        raise ValueError("%s: a cast output may only be a sink, not consumed by %s" % (dag.name, sinks_only[0].dst))
+    splits = row_splits(dag, chunking, nranks)
+    tasks = {(n.name, t): _task(n.name, t, splits[n.name]) for n in dag.nodes for t in range(splits[n.name].chunks)}
+
     for e in dag.edges:
-        src, dst = nm[e.src], nm[e.dst]
-        src_chunks, _, src_out_per = geom[src.name]
-        dst_chunks, dst_per, _ = geom[dst.name]
-        src_out = out_rows(src, nranks)
-        if node_rows(dst) > src_out:
+        src, dst = by_name[e.src], by_name[e.dst]
+        if node_rows(dst) > out_rows(src, nranks):
             raise ValueError("%s: edge %s->%s consumer reads %d rows but the producer writes %d"
-                             % (dag.name, e.src, e.dst, node_rows(dst), src_out))
+                             % (dag.name, e.src, e.dst, node_rows(dst), out_rows(src, nranks)))
         if stream_of(src.op) == stream_of(dst.op):
-            continue  # same stream: FIFO order already serialises them
-        for j in range(dst_chunks):
-            lo, hi = j * dst_per, (j + 1) * dst_per
-            hits = [k for k in range(src_chunks) if k * src_out_per < hi and (k + 1) * src_out_per > lo]
-            if not hits:
-                hits = [src_chunks - 1]
-            for k in hits:
-                if k * src_out_per >= src_out:
-                    continue
+            continue
+        ps, cs = splits[src.name], splits[dst.name]
+        for j in range(cs.chunks):
+            for k in ps.tiles_covering(j * cs.in_rows, (j + 1) * cs.in_rows):
                 tasks[(dst.name, j)]["wait"].append([src.name, k])
-                published.add((src.name, k))
-    for key in published:
-        tasks[key]["publish"] = True
+                tasks[(src.name, k)]["publish"] = True
 
     streams = {}
     for name in topo_order(dag):
-        s = stream_of(nm[name].op)
-        for i in range(geom[name][0]):
-            streams.setdefault(s, []).append(tasks[(name, i)])
+        lane = streams.setdefault(stream_of(by_name[name].op), [])
+        lane.extend(tasks[(name, t)] for t in range(splits[name].chunks))
 
     nodes = []
     for n in dag.nodes:
-        entry = {"id": n.name, "op": n.op, "engine": stream_of(n.op), "dtype": n.dtype,
-                 "tiles": geom[n.name][0], "split": geom[n.name][0] > 1,
-                 "preds": [e.src for e in dag.edges if e.dst == n.name], "iters": 1, "blocks": 1}
+        k = splits[n.name].chunks
+        entry = {"id": n.name, "op": n.op, "engine": stream_of(n.op), "dtype": n.dtype, "tiles": k,
+                 "split": k > 1, "preds": [e.src for e in dag.edges if e.dst == n.name], "iters": 1, "blocks": 1}
         entry.update(node_dims(n))
         entry.update(n.extra)
         nodes.append(entry)
@@ -258,146 +278,150 @@ def build_fixed_schedule(dag, chunking=None, nranks=1, method="fixed"):
             "chunking": {k: v for k, v in chunking.items() if v > 1}, "fallback": ""}
 
 
+# Which stream's head goes first when several could run next in the serial
+# baseline (the reference's precedence, python/kernrelay/schedule.py:67-105):
+# mixed work, then matrix, vector, CPU and collective streams; "compute" is
+# another name of "aicore".
+STREAM_PRECEDENCE = ("aicore", "aic", "aiv", "aicpu", "hccl")
+
+
+def _precedence(stream):
+    stream = "aicore" if stream == "compute" else stream
+    return STREAM_PRECEDENCE.index(stream) if stream in STREAM_PRECEDENCE else len(STREAM_PRECEDENCE)
+
+
 def serial_schedule(dag, nranks=1):
-    """Serial baseline: every tile on one ``aicore`` stream in topological order."""
+    """Serial baseline: every tile of the unsplit schedule on one ``aicore``
+    stream, no waits or publishes. The per-stream FIFOs of the unsplit
+    schedule are merged: a stream's head may go once every task it waits on
+    has gone, and of the heads that may go, the stream of highest precedence
+    goes first."""
     base = build_fixed_schedule(dag, {}, nranks=nranks, method="serial")
-    order = {"aicore": 0, "compute": 0, "aic": 1, "aiv": 2, "aicpu": 3, "hccl": 4}
-    tasks, rank, deps = {}, {}, {}
-    for engine, seq in base["streams"].items():
-        for i, t in enumerate(seq):
-            key = (t["node"], int(t.get("tile", 0)))
-            tasks[key] = t
-            rank[key] = (order.get(engine, 9), i)
-    for engine, seq in base["streams"].items():
-        for i, t in enumerate(seq):
-            key = (t["node"], int(t.get("tile", 0)))
-            d = {(w[0], int(w[1])) for w in (t.get("wait") or [])}
-            if i:
-                p = seq[i - 1]
-                d.add((p["node"], int(p.get("tile", 0))))
-            deps[key] = {x for x in d if x in tasks}
-    done, ordered = set(), []
-    while len(ordered) < len(tasks):
-        ready = [k for k in tasks if k not in done and deps[k] <= done]
-        if not ready:
-            raise RuntimeError("%s: serial baseline has a cycle" % dag.name)
-        key = min(ready, key=lambda k: rank[k])
-        ordered.append(key)
-        done.add(key)
-    merged = []
-    for key in ordered:
-        t = dict(tasks[key])
-        t["wait"] = []
-        t["publish"] = False
-        merged.append(t)
+    lanes = sorted(base["streams"].items(), key=lambda kv: _precedence(kv[0]))
+    heads = [0] * len(lanes)
+    placed, merged = set(), []
+    total = sum(len(seq) for _, seq in lanes)
+    while len(merged) < total:
+        for i, (_, seq) in enumerate(lanes):
+            if heads[i] < len(seq) and all((w[0], int(w[1])) in placed for w in seq[heads[i]].get("wait") or []):
+                t = seq[heads[i]]
+                heads[i] += 1
+                placed.add((t["node"], int(t.get("tile", 0))))
+                merged.append(dict(t, wait=[], publish=False))
+                break
+        else:
+            raise RuntimeError("%s: the serial baseline cannot order its streams (wait cycle)" % dag.name)
     out = dict(base)
-    out["streams"] = {"aicore": merged}
-    out["group"] = "serial"
-    out["chunking"] = {}
+    out.update(streams={"aicore": merged}, group="serial", chunking={})
     return out
 
 
 def validate_schedule(sched):
-    """Structural checks (the executor stays the authority). Returns errors."""
+    """Structural checks of a schedule.json dict (the executor stays the
+    authority): node ids, stream names, tasks, waits on publishing tasks and
+    a happens-before order without cycles (stream FIFO + waits). Returns the
+    list of problems found."""
     errors = []
-    nodes = sched.get("nodes") or []
-    ids = [n.get("id") for n in nodes]
+    ids = [n.get("id") for n in sched.get("nodes") or []]
     if len(ids) != len(set(ids)):
         errors.append("duplicate node ids")
-    known = set(ids)
     streams = sched.get("streams") or {}
     if not streams:
         errors.append("no streams")
-    items, seen = [], {}
+    where, publishing = {}, set()
+    before = {}  # task -> tasks that must finish first
     for engine, seq in streams.items():
         if engine not in ENGINES:
             errors.append("unknown stream %r" % engine)
         if not isinstance(seq, list):
             errors.append("stream %r is not a task list" % engine)
             continue
-        for i, t in enumerate(seq):
+        prev = None
+        for t in seq:
             key = (t.get("node"), int(t.get("tile", 0)))
-            if key[0] not in known:
+            if key[0] not in ids:
                 errors.append("stream %s task names unknown node %r" % (engine, key[0]))
-            if key in seen:
-                errors.append("node %s tile %d repeated on streams %s/%s" % (key[0], key[1], seen[key], engine))
-            seen[key] = engine
+            if key in where:
+                errors.append("node %s tile %d repeated on streams %s/%s" % (key[0], key[1], where[key], engine))
+            where[key] = engine
             if int(t.get("in_rows", 1)) <= 0:
                 errors.append("node %s tile %d has in_rows <= 0" % key)
-            items.append((key, engine, t))
-    published = {(t.get("node"), int(t.get("tile", 0))) for seq in streams.values() for t in seq
-                 if t.get("publish")}
-    pos = {item[0]: i for i, item in enumerate(items)}
-    adj = {i: set() for i in range(len(items))}
-    indeg = {i: 0 for i in range(len(items))}
-    last = {}
-    for i, (_, engine, _) in enumerate(items):
-        if engine in last:
-            adj[last[engine]].add(i)
-            indeg[i] += 1
-        last[engine] = i
-    for i, (key, _, t) in enumerate(items):
-        for w in t.get("wait") or []:
-            wkey = (w[0], int(w[1]))
-            if wkey not in pos:
-                errors.append("node %s tile %d waits on missing task %s#%s" % (key[0], key[1], wkey[0], wkey[1]))
-                continue
-            if wkey not in published:
-                errors.append("node %s tile %d waits on %s#%s which never publishes"
-                              % (key[0], key[1], wkey[0], wkey[1]))
-            j = pos[wkey]
-            if i not in adj[j]:
-                adj[j].add(i)
-                indeg[i] += 1
-    ready = [i for i, d in indeg.items() if d == 0]
-    done = 0
-    while ready:
-        cur = ready.pop()
-        done += 1
-        for nxt in adj[cur]:
-            indeg[nxt] -= 1
-            if indeg[nxt] == 0:
-                ready.append(nxt)
-    if done != len(items):
-        errors.append("schedule has a wait cycle")
+            if t.get("publish"):
+                publishing.add(key)
+            before.setdefault(key, set())
+            if prev is not None:
+                before[key].add(prev)
+            prev = key
+    for seq in streams.values():
+        for t in seq if isinstance(seq, list) else []:
+            key = (t.get("node"), int(t.get("tile", 0)))
+            for w in t.get("wait") or []:
+                dep = (w[0], int(w[1]))
+                if dep not in where:
+                    errors.append("node %s tile %d waits on missing task %s#%s" % (key[0], key[1], dep[0], dep[1]))
+                    continue
+                if dep not in publishing:
+                    errors.append("node %s tile %d waits on %s#%s which never publishes"
+                                  % (key[0], key[1], dep[0], dep[1]))
+                before[key].add(dep)
+    # a cycle in the happens-before relation: iterative three-colour DFS
+    state = {}
+    for root in before:
+        if state.get(root):
+            continue
+        stack = [(root, iter(before[root]))]
+        state[root] = 1
+        while stack:
+            node, deps = stack[-1]
+            nxt = next(deps, None)
+            if nxt is None:
+                state[node] = 2
+                stack.pop()
+            elif state.get(nxt) == 1:
+                errors.append("schedule has a wait cycle")
+                return errors
+            elif not state.get(nxt):
+                state[nxt] = 1
+                stack.append((nxt, iter(before.get(nxt, ()))))
     return errors
 
 
 def invalid_variants(sched):
-    """Deterministic broken copies of a schedule and the executor error
-    marker each must produce (reference python/kernrelay/schedule.py:185-222)."""
+    """Broken copies of a valid schedule, each paired with the error marker
+    the executor must reject it with (the four cases of the reference's E0
+    rejection gate, python/kernrelay/schedule.py:185-222, whose markers are
+    the executor's interface):
+      duplicate_engine  a second name for the mixed stream holds tasks too
+      ghost_task        a task of a node the schedule does not declare
+      wait_cycle        the first tasks of two streams wait on each other
+      row_overflow      a tile reads far past its node's rows"""
     out = {}
+    named = [k for k, v in sched["streams"].items() if v]
+
     dup = copy.deepcopy(sched)
-    first = next(k for k in dup["streams"] if dup["streams"][k])
-    dup["streams"]["compute"] = dup["streams"].pop(first)
+    moved = dup["streams"].pop(named[0])
     dup["streams"]["aicore"] = []
+    dup["streams"]["compute"] = moved
     out["duplicate_engine"] = (dup, "duplicate engine stream")
 
     ghost = copy.deepcopy(sched)
-    first = next(k for k, v in ghost["streams"].items() if v)
-    ghost["streams"][first].append({"node": "__ghost__", "tile": 0, "wait": [], "publish": False,
-                                    "in_row_off": 0, "in_rows": 1})
+    ghost["streams"][named[0]].append(
+        {"node": "__ghost__", "tile": 0, "wait": [], "publish": False, "in_row_off": 0, "in_rows": 1})
     out["ghost_task"] = (ghost, "missing plan for task")
 
-    cycle = copy.deepcopy(sched)
-    names = [k for k, v in cycle["streams"].items() if v]
-    if len(names) < 2:
-        return out
-    t0 = cycle["streams"][names[0]][0]
-    t1 = cycle["streams"][names[1]][0]
-    t0["publish"] = True
-    t1["publish"] = True
-    t0.setdefault("wait", []).append([t1["node"], int(t1.get("tile", 0))])
-    t1.setdefault("wait", []).append([t0["node"], int(t0.get("tile", 0))])
-    out["wait_cycle"] = (cycle, "wait cycle")
+    if len(named) >= 2:
+        cyc = copy.deepcopy(sched)
+        a, b = cyc["streams"][named[0]][0], cyc["streams"][named[1]][0]
+        for x, y in ((a, b), (b, a)):
+            x["publish"] = True
+            x.setdefault("wait", []).append([y["node"], int(y.get("tile", 0))])
+        out["wait_cycle"] = (cyc, "wait cycle")
 
-    over = copy.deepcopy(sched)
-    for seq in over["streams"].values():
-        for t in seq:
-            if t.get("in_row_off", 0) > 0:
-                t["in_rows"] = int(t["in_rows"]) + 10 ** 9
-                out["row_overflow"] = (over, "exceed")
-                return out
+        over = copy.deepcopy(sched)
+        later = [t for seq in over["streams"].values() for t in seq if t.get("in_row_off", 0) > 0]
+        if later:
+            later[0]["in_rows"] = int(later[0]["in_rows"]) + 10 ** 9
+            out["row_overflow"] = (over, "exceed")
     return out
 
 

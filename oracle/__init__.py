@@ -14,6 +14,9 @@ Modules
               (exec/qwen_main.cpp:925-992) over a model directory
   dag_eval    node outputs of a schedule.json's DAG (first rows or full)
   relay_model a CPU thread model of the device flag protocol
+  hf_reference transformers' Qwen2/Qwen3ForCausalLM on a model directory:
+              the independent writer of ref_last_logits.bin / ref.json and
+              the pin of qwen's composition
 
 How each function is pinned (golden vectors, closed forms, brute force,
 library routines) is listed in each module header; tests/test_oracle_*.py

@@ -8,8 +8,13 @@ names of scripts/export_model.py:142-204 (matmul weights stored as weight_t
 residual stream alternates h0/h1 exactly as the reference's buffers do.
 
 Pinned against transformers' Qwen2ForCausalLM / Qwen3ForCausalLM built from
-a local config at tiny shapes (tests/test_oracle_qwen.py): same logits within
-bf16 tolerance and the same argmax.
+a local config and loaded with the same model directory
+(oracle/hf_reference.py), at tiny shapes covering QKV bias + GQA + tied
+lm_head and q/k-norm + untied lm_head (tests/test_oracle_qwen.py): last-row
+logits within 2e-2 + 1e-2|ref| at the default init and within 3e-2 max|ref|
+at a wide init, the same argmax, and nine planted composition mistakes
+(residual, bias, RoPE sign or skip, GQA mapping, scale, gate/up order, norm
+gain, eps) each rejected by more than 10x that bound.
 """
 
 import json

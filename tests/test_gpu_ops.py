@@ -525,3 +525,79 @@ def _streamk_case(M, N, K, bias):
     ops.gemm(A, Bt, dp, bias=b)
     close(C, dp)
     close(C, O.gemm(A.cpu(), Bt.cpu().t(), bias=b.cpu() if bias else None))
+
+
+@pytest.mark.parametrize("M,N,K,k,streamk", [(2048, 3584, 3584, 1, False), (2048, 3584, 3584, 4, False),
+                                             (2048, 3584, 18944, 8, False), (2048, 896, 4864, 4, True),
+                                             (2048, 896, 4864, 2, False), (256, 256, 512, 4, False),
+                                             (512, 4096, 1024, 2, False)])
+def test_gemm_add_rmsnorm_relay_bit_exact(gpu, M, N, K, k, streamk):
+    """The row-tiled relay of a projection to its Add+RMSNorm consumer: the
+    GEMM releases k row tiles and its own workgroups normalise each released
+    tile. y, the residual sum and rstd equal the GEMM followed by the
+    standalone Add+RMSNorm kernel bit for bit (the 7B o and down shapes, the
+    Qwen2.5-0.5B down shape with its four-piece K split, 64-row tiles); every
+    relay tile's block ends with published == consumed == runs and status 1
+    over repeated runs without a host reset; y matches the oracle's
+    Add+RMSNorm of the stored product."""
+    announce("gemm+add_rmsnorm relay %dx%dx%d k=%d streamk=%s" % (M, N, K, k, streamk))
+    g = torch.Generator(device="cuda").manual_seed(60)
+    A = torch.randn(M, K, device="cuda", generator=g).to(torch.bfloat16)
+    Bt = (torch.randn(N, K, device="cuda", generator=g) * 0.02).to(torch.bfloat16)
+    res = torch.randn(M, N, device="cuda", generator=g).to(torch.bfloat16)
+    gamma = (1.0 + 0.1 * torch.randn(N, device="cuda", generator=g)).to(torch.bfloat16)
+    ws = cnt = None
+    if streamk:
+        nb, nc = ops.gemm_streamk_workspace(M, N, K)
+        assert nb > 0
+        ws = torch.empty(nb, dtype=torch.uint8, device="cuda")
+        cnt = torch.zeros(nc, dtype=torch.int32, device="cuda")
+    ref_c = torch.empty(M, N, dtype=torch.bfloat16, device="cuda")
+    if streamk:
+        ops.gemm_streamk(A, Bt, ref_c, ws, cnt)
+    else:
+        ops.gemm(A, Bt, ref_c)
+    ref_y, ref_s = torch.empty_like(ref_c), torch.empty_like(ref_c)
+    ref_r = torch.empty(M, dtype=torch.float32, device="cuda")
+    ops.rowop("add_rmsnorm", res, ref_y, x1=ref_c, gamma=gamma, sum_out=ref_s, rstd_out=ref_r)
+    torch.cuda.synchronize()
+    ctrl = torch.zeros(k * ops.CTRL_WORDS, dtype=torch.int32, device="cuda")
+    C, y, s = torch.empty_like(ref_c), torch.empty_like(ref_c), torch.empty_like(ref_c)
+    rstd = torch.empty_like(ref_r)
+    runs = 3
+    for _ in range(runs):
+        for t in (C, y, s, rstd):
+            t.zero_()
+        ops.gemm_add_rmsnorm(A, Bt, C, res, gamma, y, ops.make_pub(ctrl, 0, M // k), sum_out=s, rstd=rstd,
+                             ws=ws, counters=cnt)
+        torch.cuda.synchronize()
+        assert torch.equal(C, ref_c)
+        assert torch.equal(y, ref_y) and torch.equal(s, ref_s) and torch.equal(rstd, ref_r)
+    blk = ctrl.cpu().reshape(k, ops.CTRL_WORDS)
+    assert torch.all(blk[:, 0] == runs) and torch.all(blk[:, 1] == runs)   # published == consumed
+    assert torch.all(blk[:, 2] == 1)                                        # status ok
+    assert torch.all(blk[:, 3] == 0) and torch.all(blk[:, 4] == 0)          # tickets reset
+    if cnt is not None:
+        assert int(cnt.abs().sum()) == 0
+    rows = torch.arange(0, M, max(1, M // 64))
+    oy, osum, _ = O.add_rmsnorm(res[rows].float().cpu(), ref_c[rows].float().cpu(), gamma.float().cpu(), 1e-6)
+    close(y[rows], oy)
+    assert torch.equal(s[rows].float().cpu(), osum)
+
+
+def test_gemm_add_rmsnorm_relay_refuses_unresident_tiles(gpu):
+    """A relay tile whose producer workgroups cannot all be resident at once
+    (8192 rows x 4096 columns in one tile: 512 workgroups of 256x256 against
+    256 CUs) is refused before anything is launched: its consumer would wait
+    on workgroups not yet placed."""
+    M, N, K = 8192, 4096, 512
+    A = torch.zeros(M, K, dtype=torch.bfloat16, device="cuda")
+    Bt = torch.zeros(N, K, dtype=torch.bfloat16, device="cuda")
+    C = torch.empty(M, N, dtype=torch.bfloat16, device="cuda")
+    res, y = torch.empty_like(C), torch.empty_like(C)
+    gamma = torch.ones(N, dtype=torch.bfloat16, device="cuda")
+    ctrl = torch.zeros(ops.CTRL_WORDS, dtype=torch.int32, device="cuda")
+    with pytest.raises(RuntimeError, match="do not fit the device at once"):
+        ops.gemm_add_rmsnorm(A, Bt, C, res, gamma, y, ops.make_pub(ctrl, 0, M))
+    torch.cuda.synchronize()
+    assert int(ctrl.abs().sum()) == 0

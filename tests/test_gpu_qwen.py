@@ -1,6 +1,18 @@
 """kr_qwen_run on the GPU: every mode produces bit-identical logits (the
 relay split does not change any reduction), the last-token logits match the
-fp32 CPU oracle (|d| <= 2e-2 + 1e-2|ref|) and its argmax."""
+fp32 CPU oracle within |d| <= 2e-2 + 1e-2 |ref| and the argmax is the
+oracle's, asserted always.
+
+Seeds are chosen so that the oracle's top-2 logit margin clears the error
+bound (each test names its seed and the margin measured by the oracle): a
+deviation within the bound cannot swap the top two logits.
+
+Reference files (ref_last_logits.bin, ref.json) of the tiny models are
+written by transformers (oracle/hf_reference.py, as the reference's exporter
+writes them from HF logits, scripts/export_model.py:211-223), so the
+runtime's own Verify (ref_argmax, maxdiff) checks against a model that shares
+no code with the oracle; the larger shapes use the oracle's files.
+"""
 
 import os
 
@@ -9,6 +21,7 @@ import pytest
 import torch
 
 from kernrelay_amd import libapi, modeldir
+from oracle import hf_reference as hf
 from oracle import qwen as oq
 from tests.conftest import announce
 
@@ -16,11 +29,34 @@ pytestmark = pytest.mark.gpu
 
 MODES = ["serial", "serial_fused", "serial_graph", "graph_whole", "relay_event", "relay_flag",
          "relay_flag_graph", "relay_split:1", "relay_split:2", "relay_split:4"]
+ATOL, RTOL = 2e-2, 1e-2
+# Two-layer model-shape tests (Qwen2.5-0.5B / 7B / Qwen3-8B sizes, ~152k
+# logits). The fp32 oracle's own logits move by more than 2e-2 under changes
+# that any bf16 GPU implementation makes, measured on the CPU with the same
+# model directories:
+#                                   0.5B seed 3      7B seed 2
+#   GEMMs accumulated in fp64       0.0234 (0.0037)  0.0469 (0.0076)
+#   P rounded to bf16 before P.V    0.0234 (0.0039)  0.0625 (0.0092)
+# (max |d|, mean in brackets). The kernels accumulate in fp32 in their own
+# order and round P to bf16 for the MFMA, so the bound for these tests is
+# the larger of the two with room: 3e-2 (0.5B) and 8e-2 (7B, 8B) absolute
+# plus 1e-2 |ref|, and the mean deviation at most 1.5e-2. The argmax is
+# asserted with a margin above twice the largest deviation.
+MODEL_BOUND = {"qwen2.5-0.5b": 3e-2, "qwen2.5-7b": 8e-2, "qwen3-8b": 8e-2}
+MODEL_MEAN = 1.5e-2
 
 
-def make(tmp, preset, seq, layers=None):
-    d = modeldir.write_model_dir(tmp / preset, preset, seq=seq, layers=layers)
-    ref = oq.write_reference(d)
+def make(tmp, preset, seq, layers=None, seed=1234, hf_ref=False):
+    announce("write model dir %s seq=%d layers=%s seed=%d" % (preset if isinstance(preset, str) else "custom",
+                                                            seq, layers, seed))
+    name = preset if isinstance(preset, str) else "custom"
+    d = modeldir.write_model_dir(tmp / name, preset, seq=seq, layers=layers, seed=seed)
+    ref = oq.prefill(d)
+    if hf_ref:
+        r_hf = hf.write_reference(d)
+        assert r_hf["argmax"] == ref["argmax"], (r_hf["argmax"], ref["argmax"])
+    else:
+        oq.write_reference(d, result=ref)
     return d, ref
 
 
@@ -36,20 +72,33 @@ def run(d, mode, seq, dump=None, iters=2):
     return r
 
 
-def check_logits(dump, ref, atol=2e-2):
+def check_logits(dump, ref, atol=ATOL, rtol=RTOL, mean_tol=None):
+    """Last-row logits within atol + rtol |ref| of the oracle's (and on
+    average within mean_tol), same argmax; returns the largest deviation."""
     w = np.fromfile(dump / "last_logits_bf16.bin", dtype=np.uint16)
     g = torch.from_numpy(w.view(np.int16).copy()).view(torch.bfloat16).double()
     r = ref["last_logits"].double()
     err = (g - r).abs()
-    assert bool((err <= atol + 1e-2 * r.abs()).all()), float(err.max())
-    if ref["margin"] > 4e-2:
-        assert int(g.argmax()) == ref["argmax"]
+    bound = atol + rtol * r.abs()
+    i = int((err - bound).argmax())
+    announce("max |gpu - oracle| = %.4g, mean %.4g (bound at the argmax %.4g, margin %.4g)" % (
+        float(err.max()), float(err.mean()), float(bound[ref["argmax"]]), ref["margin"]))
+    assert bool((err <= bound).all()), "max err %.4g at %d (ref %.4g gpu %.4g)" % (float(err.max()), i, float(r[i]),
+                                                                                   float(g[i]))
+    if mean_tol is not None:
+        assert float(err.mean()) <= mean_tol, float(err.mean())
+    # the seed's margin clears the deviations: the argmax cannot move within them
+    assert ref["margin"] > 2 * float(err.max()), ("seed's margin too small", ref["margin"], float(err.max()))
+    assert int(g.argmax()) == ref["argmax"], (int(g.argmax()), ref["argmax"])
+    return float(err.max())
 
 
 @pytest.mark.parametrize("preset", ["tiny-qwen2", "tiny-qwen3"])
 def test_all_modes_bit_exact_and_match_oracle(gpu, tmp_path, preset):
+    """Seed 1234: oracle margins 0.375 (tiny-qwen2) and 0.320 (tiny-qwen3);
+    reference files from transformers."""
     seq = 256
-    d, ref = make(tmp_path, preset, seq)
+    d, ref = make(tmp_path, preset, seq, hf_ref=True)
     fnv = None
     for mode in MODES:
         dump = tmp_path / ("dump_" + mode.replace(":", "_"))
@@ -74,8 +123,7 @@ def test_split_k_down_all_modes_bit_exact(gpu, tmp_path):
     cfg["intermediate_size"] = 8192
     seq = 512
     assert ops.gemm_streamk_workspace(seq, cfg["hidden_size"], 8192)[0] > 0  # the down GEMM splits
-    d = modeldir.write_model_dir(tmp_path / "splitk", cfg, seq=seq)
-    ref = oq.write_reference(d)
+    d, ref = make(tmp_path, cfg, seq, seed=7)  # oracle margin 0.320
     fnv = None
     os.environ["KR_QWEN_SPLITK"] = "1"
     try:
@@ -100,8 +148,7 @@ def test_rope_epilogue_bit_exact(gpu, tmp_path, head_dim):
     cfg = dict(modeldir.PRESETS["tiny-qwen2"])
     cfg.update(hidden_size=512, num_attention_heads=4, num_key_value_heads=2, head_dim=head_dim)
     seq = 512
-    d = modeldir.write_model_dir(tmp_path / ("rope%d" % head_dim), cfg, seq=seq)
-    ref = oq.write_reference(d)
+    d, ref = make(tmp_path / ("rope%d" % head_dim), cfg, seq)  # margins 0.359 (D 64), 0.867 (D 128)
     fnv = {}
     for epi in ("0", "1"):
         os.environ["KR_QWEN_ROPE_EPI"] = epi
@@ -119,24 +166,23 @@ def test_rope_epilogue_bit_exact(gpu, tmp_path, head_dim):
 
 def test_qwen05_shapes_split_bit_exact(gpu, tmp_path):
     """Qwen2.5-0.5B layer shapes (H 896, 14/2 heads, D 64, I 4864, V 151936,
-    tied) at seq 2048, two layers: serial == relay_split:4 (SwiGLU in the
-    gate/up epilogue, and flag-released), oracle argmax. The logit bound's
-    floor is 3e-2 here: the largest of 151936 bf16 logits' deviations from
-    the fp32 oracle measured 0.0234 on MI355X whether the down projection
-    splits K or not (mean 0.0039 both ways; 4 layers: 0.032 unsplit, 0.031
-    split), one bf16 step away from the 2e-2 floor of the 2048-entry
-    vocabularies."""
+    tied; the down projection splits K in four) at seq 2048, two layers, seed
+    3 (oracle margin 0.5625): serial == relay_split:k for every k (SwiGLU in
+    the gate/up epilogue, o and down releasing their row tiles to the
+    Add+RMSNorm consumers), and the flag-released SwiGLU variant; the oracle's
+    logits within the bound and its argmax."""
     seq = 2048
-    d, ref = make(tmp_path, "qwen2.5-0.5b", seq, layers=2)
+    d, ref = make(tmp_path, "qwen2.5-0.5b", seq, layers=2, seed=3)
     dump = tmp_path / "dump"
     dump.mkdir()
     a = run(d, "graph_whole", seq, dump)
-    check_logits(dump, ref, atol=3e-2)
-    b = run(d, "relay_split:4", seq)
-    assert a["logits_fnv64"] == b["logits_fnv64"]
-    assert b["flag_timeouts"] == 0
-    # the flag-released variant: SwiGLU workgroups appended to the gate/up
-    # GEMM wait on its 4 row tiles
+    check_logits(dump, ref, atol=MODEL_BOUND["qwen2.5-0.5b"], mean_tol=MODEL_MEAN)
+    for k in (1, 2, 4, 8):
+        b = run(d, "relay_split:%d" % k, seq)
+        assert a["logits_fnv64"] == b["logits_fnv64"], k
+        assert b["flag_timeouts"] == 0
+    # the flag-released SwiGLU variant: SwiGLU workgroups appended to the
+    # gate/up GEMM wait on its 4 row tiles
     os.environ["KR_SPLIT_SWIGLU"] = "flags"
     try:
         c = run(d, "relay_split:4", seq)
@@ -144,6 +190,58 @@ def test_qwen05_shapes_split_bit_exact(gpu, tmp_path):
         del os.environ["KR_SPLIT_SWIGLU"]
     assert a["logits_fnv64"] == c["logits_fnv64"]
     assert c["flag_timeouts"] == 0 and c["flag_edges"] > 0
+
+
+def _large_shapes(tmp_path, preset, seq, seed):
+    d, ref = make(tmp_path, preset, seq, layers=2, seed=seed)
+    dump = tmp_path / "dump"
+    dump.mkdir()
+    a = run(d, "graph_whole", seq, dump, iters=1)
+    check_logits(dump, ref, atol=MODEL_BOUND[preset], mean_tol=MODEL_MEAN)
+    assert a["ref_argmax"] == ref["argmax"]
+    for k in (1, 2, 4, 8):
+        b = run(d, "relay_split:%d" % k, seq, iters=1)
+        assert b["logits_fnv64"] == a["logits_fnv64"], k
+        assert b["flag_timeouts"] == 0 and b["argmax"] == ref["argmax"]
+    return a
+
+
+def test_qwen25_7b_shapes(gpu, tmp_path):
+    """Qwen2.5-7B layer shapes (H 3584, 28/4 heads, D 128, QKV bias, I 18944,
+    V 152064, untied lm_head) at seq 2048, two layers, seed 2 (oracle margin
+    0.344): the QKV GEMM with 192-row tiles, bias and the RoPE epilogue, the
+    gate/up GEMM 2048x37888x3584 with and without its SwiGLU epilogue, the
+    down projection and lm_head at N 152064 against the oracle; serial ==
+    relay_split:k for k = 1, 2, 4, 8 bit for bit."""
+    _large_shapes(tmp_path, "qwen2.5-7b", 2048, seed=2)
+
+
+def test_qwen3_8b_shapes(gpu, tmp_path):
+    """Qwen3-8B text shapes (H 4096, 32/8 heads, D 128, q/k RMSNorm, no bias,
+    I 12288, V 151936, untied) at seq 4096, two layers, seed 1234 (oracle margin 0.281): the
+    q/k-norm path, attention over 4096 positions and the 4096-row GEMMs
+    against the oracle; serial == relay_split:k bit for bit."""
+    _large_shapes(tmp_path, "qwen3-8b", 4096, seed=1234)
+
+
+def test_lm_head_vocab_152064(gpu):
+    """The lm_head GEMM at its real size, [2048, 3584] x [3584, 152064], rows
+    spread over the M tiles against the oracle (all 152064 columns)."""
+    from kernrelay_amd import ops
+    from oracle import ops as O
+    M, K, N = 2048, 3584, 152064
+    announce("lm_head gemm %dx%dx%d" % (M, N, K))
+    g = torch.Generator().manual_seed(11)
+    A = (torch.randn(M, K, generator=g)).to(torch.bfloat16)
+    Bt = (torch.randn(N, K, generator=g) * 0.02).to(torch.bfloat16)
+    C = torch.empty(M, N, dtype=torch.bfloat16, device="cuda")
+    ops.gemm(A.cuda(), Bt.cuda(), C)
+    torch.cuda.synchronize()
+    rows = torch.tensor([0, 1, 255, 256, 777, 1023, 1024, 1500, 1791, 2046, 2047])
+    ref = O.gemm(A[rows].float(), Bt.float().t())
+    got = C[rows.cuda()].float().cpu()
+    err = (got - ref).abs()
+    assert bool((err <= ATOL + RTOL * ref.abs()).all()), float(err.max())
 
 
 def test_profile_many(gpu, tmp_path):

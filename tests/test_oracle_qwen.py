@@ -1,0 +1,152 @@
+"""Pin the Qwen prefill oracle (oracle/qwen.py) against transformers.
+
+oracle.qwen composes the pinned ops in the reference's BuildSerial order
+(exec/qwen_main.cpp:925-992, EmitQkv :1336-1344, EmitQkNorm :1346-1357).
+The composition itself — residual order, q/k-norm before RoPE, bias before
+RoPE, GQA head mapping, SwiGLU order, final norm, tied or untied lm_head —
+is checked here against transformers' Qwen2ForCausalLM / Qwen3ForCausalLM
+built from a local config and loaded with the same model directory
+(oracle/hf_reference.py; nothing is fetched).
+
+Two architectures cover the reference's variants: tiny-qwen2 (QKV bias, GQA
+4/2, head_dim 64, tied lm_head) and tiny-qwen3 (q/k RMSNorm, no bias, GQA
+4/2, head_dim 128, untied lm_head).
+
+Tolerances. transformers runs in fp32; the oracle rounds every stored
+activation to bf16 and uses the bf16 RoPE tables of the model directory, so
+the two differ by bf16 rounding noise, which grows with the activations:
+  * default init (std 0.02, the init every GPU test uses): within the
+    north_star bound |d| <= 2e-2 + 1e-2 |ref| (measured 0.35 and 0.80 of it);
+  * wide init (weights std 0.05, norm gains 1 + N(0, 0.3), so that a dropped
+    or misplaced gain moves the logits): |d| <= 3e-2 max|ref| (measured 0.012
+    and 0.015 of max|ref|), the same argmax.
+Each planted mistake below, put into the oracle on the CPU, moves the logits
+by more than 0.3 max|ref| at the wide init (measured 0.34 to 1.5), so the
+3e-2 bound separates a correct composition from each by over 10x.
+"""
+
+import contextlib
+
+import numpy as np
+import pytest
+import torch
+
+from kernrelay_amd import modeldir
+from oracle import hf_reference as hf
+from oracle import ops as O
+from oracle import qwen as oq
+
+PRESETS = ["tiny-qwen2", "tiny-qwen3"]
+SEQ = 128
+WIDE = dict(std=0.05, gain_std=0.3)
+WIDE_TOL = 3e-2
+
+
+@pytest.fixture(scope="module")
+def dirs(tmp_path_factory):
+    root = tmp_path_factory.mktemp("hfpin")
+    out = {}
+    for p in PRESETS:
+        out[(p, "default")] = modeldir.write_model_dir(root / (p + "_default"), p, seq=SEQ)
+        out[(p, "wide")] = modeldir.write_model_dir(root / (p + "_wide"), p, seq=SEQ, **WIDE)
+    return out
+
+
+@pytest.fixture(scope="module")
+def hf_logits(dirs):
+    return {k: hf.last_logits(d, torch.float32) for k, d in dirs.items()}
+
+
+@pytest.mark.parametrize("preset", PRESETS)
+def test_oracle_matches_transformers_default_init(dirs, hf_logits, preset):
+    ref = hf_logits[(preset, "default")]
+    got = oq.prefill(dirs[(preset, "default")])
+    err = (got["last_logits"] - ref).abs()
+    assert bool((err <= 2e-2 + 1e-2 * ref.abs()).all()), float(err.max())
+    assert got["argmax"] == int(ref.argmax())
+
+
+@pytest.mark.parametrize("preset", PRESETS)
+def test_oracle_matches_transformers_wide_init(dirs, hf_logits, preset):
+    ref = hf_logits[(preset, "wide")]
+    got = oq.prefill(dirs[(preset, "wide")])
+    err = float((got["last_logits"] - ref).abs().max())
+    assert err <= WIDE_TOL * float(ref.abs().max()), err
+    assert got["argmax"] == int(ref.argmax())
+
+
+# --- planted mistakes (in the oracle, on the CPU) ---------------------------
+
+_ORIG = {n: getattr(O, n) for n in ("gemm", "rope", "add_rmsnorm", "attention", "swiglu", "rmsnorm")}
+
+
+def _gqa_tiled(q, k, v, scale=None, dt=torch.bfloat16):
+    # query head h reads kv head h % HKV instead of h // (HQ / HKV)
+    rep = q.shape[1] // k.shape[1]
+    return _ORIG["attention"](q, k.repeat(1, rep, 1), v.repeat(1, rep, 1), scale, dt)
+
+
+MISTAKES = {
+    "residual dropped": dict(add_rmsnorm=lambda a, b, g, eps, dt=torch.bfloat16:
+                             _ORIG["add_rmsnorm"](torch.zeros_like(b), b, g, eps, dt)),
+    "bias dropped": dict(gemm=lambda a, w, bias=None, dt=torch.bfloat16: _ORIG["gemm"](a, w, None, dt)),
+    "rope sign flipped": dict(rope=lambda x, c, s, dt=torch.bfloat16: _ORIG["rope"](x, c, -s, dt)),
+    "rope skipped": dict(rope=lambda x, c, s, dt=torch.bfloat16: x),
+    "gqa heads tiled": dict(attention=_gqa_tiled),
+    "attention scale 1/D": dict(attention=lambda q, k, v, scale=None, dt=torch.bfloat16:
+                                _ORIG["attention"](q, k, v, 1.0 / q.shape[-1], dt)),
+    "gate and up swapped": dict(swiglu=lambda g, u, dt=torch.bfloat16: _ORIG["swiglu"](u, g, dt)),
+    "norm gain dropped": dict(rmsnorm=lambda x, g, eps, dt=torch.bfloat16:
+                              _ORIG["rmsnorm"](x, torch.ones_like(g), eps, dt)),
+    "norm eps 1e-2": dict(rmsnorm=lambda x, g, eps, dt=torch.bfloat16: _ORIG["rmsnorm"](x, g, 1e-2, dt)),
+}
+
+
+@contextlib.contextmanager
+def planted(name):
+    patch = MISTAKES[name]
+    for k, v in patch.items():
+        setattr(O, k, v)
+    try:
+        yield
+    finally:
+        for k in patch:
+            setattr(O, k, _ORIG[k])
+
+
+@pytest.mark.parametrize("preset", PRESETS)
+@pytest.mark.parametrize("mistake", sorted(MISTAKES))
+def test_planted_mistake_fails_the_pin(dirs, hf_logits, preset, mistake):
+    if mistake == "bias dropped" and preset == "tiny-qwen3":
+        pytest.skip("tiny-qwen3 has no QKV bias")
+    ref = hf_logits[(preset, "wide")]
+    with planted(mistake):
+        got = oq.prefill(dirs[(preset, "wide")])["last_logits"]
+    err = float((got - ref).abs().max())
+    # the pin's bound rejects it, with room to spare
+    assert err > 5 * WIDE_TOL * float(ref.abs().max()), (mistake, err)
+
+
+def test_pin_restores_the_oracle(dirs, hf_logits):
+    """The patches leave the oracle as it was (the checks above are independent)."""
+    for n, f in _ORIG.items():
+        assert getattr(O, n) is f
+
+
+# --- the independent reference-logits writer --------------------------------
+
+@pytest.mark.parametrize("preset", PRESETS)
+def test_hf_writer_writes_reference_files(dirs, hf_logits, preset):
+    """ref_last_logits.bin / ref.json as the reference's exporter writes them
+    (export_model.py:211-223), from transformers rather than the oracle."""
+    import json
+    d = dirs[(preset, "default")]
+    res = hf.write_reference(d)
+    raw = np.fromfile(d / "ref_last_logits.bin", dtype=np.float32)
+    meta = json.loads((d / "ref.json").read_text())
+    assert raw.shape == (int(json.loads((d / "manifest.json").read_text())["config"]["vocab_size"]),)
+    assert np.array_equal(raw, hf_logits[(preset, "default")].numpy())
+    assert meta["argmax_last"] == int(raw.argmax()) == res["argmax"]
+    assert meta["source"].startswith("transformers")
+    # the writer's argmax agrees with the oracle's
+    assert meta["argmax_last"] == oq.prefill(d)["argmax"]
