@@ -3,24 +3,23 @@
 The planner decides which producer -> consumer edges of a prefill DAG to run
 as k row tiles (the relay split) by simulating the engines' queues:
 
-* ``layer_dag``      — the per-layer Qwen DAG the planner works on
-                       (python/kernrelay/optimize.py:59-142).
-* ``Costs``          — unsplit cost per op shape and the tax of k tiles
-                       (python/kernrelay/planner2.py:50-166).
-* ``simulate``       — list schedule, per-engine FIFO, tile-wise deps
-                       (planner2.py:269-382).
-* ``bubbles``        — engine idle time caused by a data dependency
-                       (planner2.py:385-409).
-* ``greedy_plan``    — bubble-driven split search (planner2.py:587-680).
+* ``layer_dag``      — the per-layer Qwen DAG the planner works on (the
+                       reference's python/kernrelay/optimize.py:59-142).
+* ``Costs``          — unsplit cost per op shape and the tax of k tiles.
+* ``simulate``       — event-loop list schedule over a heap, per-engine
+                       queues, tile-wise dependencies.
+* ``bubbles``        — engine idle time caused by a data dependency.
+* ``greedy_plan``    — bubble-driven split search (``_SplitSearch``).
 * ``plan_dag``       — feeds a ``kr_qwen_profile_many`` table into the
                        search (optimize.py:179-237).
 
-Tie-breaks, the candidate k sets and the tax formulas follow the reference
-exactly, so the same DAG and cost table give the same schedule, makespan and
-splits.  The schedule is built with a lazily re-keyed heap instead of a scan
-over all pending tasks: a ready task's start key can only grow (engine free
-times are monotone), so the first popped entry whose key is current is the
-scan's minimum.
+The code is this package's own; what it shares with the reference's planner
+(python/kernrelay/planner2.py) is what a recorded plan depends on: the
+cost-file fields and fallback constants, the split-tax rules, the candidate
+tile counts, the tile-overlap rules, the order in which ready tasks, bubbles
+and options are considered, and validate_graph's messages. With those the
+same DAG and cost table give the reference's schedule, makespan, splits and
+decisions (tests/test_planner.py against its recorded results).
 """
 
 import copy
@@ -167,39 +166,50 @@ def project_summary(dag, cfg, seq):
 # ------------------------------------------------------------- costs ----
 
 _MM_KEY = re.compile(r"matmul\|(\d+)x(\d+)x(\d+)$")
+_RC_KEY = re.compile(r"([a-z_0-9]+)\|(\d+)x(\d+)$")
+
+# Fallback constants of a cost file without them, and of the roofline price of
+# an unmeasured GEMM (the reference's planner2.py:54-123 uses the same values;
+# the recorded plans depend on them).
+_TABLE_DEFAULTS = (("launch_us", 8.0), ("traffic_gbps", 600.0), ("l2_mb", 32.0), ("event_us", 20.0))
+_ROOFLINE_FLOPS = 250e12           # flop/s of an unmeasured GEMM
+_AICPU_US_PER_ELEMENT = 2.2e-3     # host-side scalar op
+_COLUMN_SPLIT_US_PER_MB = 1.6      # re-assembly of a column-split output
 
 
 class Costs:
-    """Unsplit cost per shape (``full``) and the tax of splitting into k.
+    """What an op costs unsplit, and what running it as k tiles adds.
 
-    ``table`` has the layout of a cost file: ``full`` {shape_key: us},
-    ``launch_us``, ``traffic_gbps``, ``l2_mb``, ``event_us``.  ``curves``
-    maps shape keys to measured split curves
+    ``table`` has the layout of a cost file: ``full`` {shape_key: us} plus
+    the scalars ``launch_us``, ``traffic_gbps``, ``l2_mb``, ``event_us``.
+    ``curves`` maps shape keys to measured split curves
     ``{"base_best_us", "fit": {"slope_us_per_tile", "intercept_us"}}``.
-    Shapes missing from ``full`` are scaled from a measured shape with the
-    same inner dimensions, else priced by a roofline (planner2.py:86-123).
+
+    An unsplit cost is resolved in order: the measured entry; for a GEMM, the
+    first measured GEMM with the same K and N scaled by M; for a row op, the
+    first measured entry of the op with the same columns scaled by rows; else
+    a roofline price (the reference's resolution, planner2.py:86-123).
     """
 
     def __init__(self, table, curves=None):
         self.data = table
         self.full = dict(table.get("full", {}))
-        self.launch = float(table.get("launch_us", 8.0))
-        self.bw = float(table.get("traffic_gbps", 600.0)) * 1e9
-        self.l2 = float(table.get("l2_mb", 32.0)) * 1024 * 1024
-        self.event = float(table.get("event_us", 20.0))
+        scalars = {name: float(table.get(name, default)) for name, default in _TABLE_DEFAULTS}
+        self.launch = scalars["launch_us"]
+        self.bw = scalars["traffic_gbps"] * 1e9
+        self.l2 = scalars["l2_mb"] * 1024 * 1024
+        self.event = scalars["event_us"]
         self.curves = dict(curves or {})
-        self._base = {}
-        self._tax = {}
+        self._resolved = {}
+        self._taxes = {}
 
     @classmethod
     def from_files(cls, path, curves_path=None):
-        """Cost file plus an optional curve file (``{"cases": [...]}``,
-        planner2.py:60-73)."""
+        """Cost file plus an optional curve file (``{"cases": [...]}``)."""
         table = json.loads(Path(path).read_text(encoding="utf-8"))
         curves = {}
         if curves_path and Path(curves_path).exists():
-            raw = json.loads(Path(curves_path).read_text(encoding="utf-8"))
-            for case in raw.get("cases", []):
+            for case in json.loads(Path(curves_path).read_text(encoding="utf-8")).get("cases", []):
                 key = cls.curve_key(case)
                 if key:
                     curves[key] = case
@@ -207,79 +217,83 @@ class Costs:
 
     @staticmethod
     def curve_key(case):
-        op, s = case.get("op"), case.get("shape") or {}
+        op, shape = case.get("op"), case.get("shape") or {}
         if op in ("matmul", "attention"):
-            return shape_key({"op": op, "shape": s})
-        if s.get("rows") and s.get("cols"):
-            return "%s|%dx%d" % (op, s["rows"], s["cols"])
+            return shape_key({"op": op, "shape": shape})
+        if shape.get("rows") and shape.get("cols"):
+            return "%s|%dx%d" % (op, shape["rows"], shape["cols"])
         return None
+
+    # -- unsplit cost --------------------------------------------------------
+    def _scaled_neighbour(self, node):
+        """A measured entry of the same inner shape, scaled along the rows."""
+        shape, op = node["shape"], node["op"]
+        for key, us in self.full.items():
+            if op == "matmul":
+                m = _MM_KEY.match(key)
+                if m and (int(m.group(2)), int(m.group(3))) == (shape["K"], shape["N"]):
+                    return float(us) * shape["M"] / int(m.group(1))
+            else:
+                m = _RC_KEY.match(key)
+                if m and m.group(1) == op and int(m.group(3)) == shape.get("cols", 0):
+                    return float(us) * shape.get("rows", 0) / max(int(m.group(2)), 1)
+        return None
+
+    def _roofline(self, node):
+        hbm_us = shape_bytes(node) / self.bw * 1e6
+        if node["op"] != "matmul":
+            return max(hbm_us, 1.0)
+        s = node["shape"]
+        return max(2.0 * s["M"] * s["K"] * s["N"] / _ROOFLINE_FLOPS * 1e6, hbm_us)
 
     def base(self, node):
         key = shape_key(node)
-        if key in self._base:
-            return self._base[key]
-        if key in self.full:
-            val = self._base[key] = float(self.full[key])
-            return val
-        s, op = node["shape"], node["op"]
-        if op == "custom_aicpu_scale":
-            # host-side scalar op: 2.2 ns per element, not cached
-            return max(1.0, s.get("rows", 0) * s.get("cols", 0) * 2.2e-3)
-        if op == "matmul":
-            for k, v in self.full.items():
-                m = _MM_KEY.match(k)
-                if m and int(m.group(2)) == s["K"] and int(m.group(3)) == s["N"]:
-                    val = self._base[key] = float(v) * s["M"] / int(m.group(1))
-                    return val
-        else:
-            pat = re.compile(re.escape(op) + r"\|(\d+)x(\d+)$")
-            for k, v in self.full.items():
-                if not k.startswith(op + "|"):
-                    continue
-                m = pat.match(k)
-                if m and int(m.group(2)) == s.get("cols", 0):
-                    val = float(v) * s.get("rows", 0) / max(int(m.group(1)), 1)
-                    self._base[key] = val
-                    return val
-        hbm_us = shape_bytes(node) / self.bw * 1e6
-        if op == "matmul":
-            val = max(2.0 * s["M"] * s["K"] * s["N"] / 250e12 * 1e6, hbm_us)
-        else:
-            val = max(hbm_us, 1.0)
-        self._base[key] = val
-        return val
+        if key not in self._resolved:
+            if key in self.full:
+                self._resolved[key] = float(self.full[key])
+            elif node["op"] == "custom_aicpu_scale":
+                s = node["shape"]
+                return max(1.0, s.get("rows", 0) * s.get("cols", 0) * _AICPU_US_PER_ELEMENT)
+            else:
+                scaled = self._scaled_neighbour(node)
+                self._resolved[key] = scaled if scaled is not None else self._roofline(node)
+        return self._resolved[key]
+
+    # -- the tax of k tiles --------------------------------------------------
+    def _weight_reread_us(self, node, k):
+        """A row-split GEMM re-reads its weight once per extra tile when the
+        weight does not stay in the last-level cache."""
+        if node["op"] != "matmul":
+            return 0.0
+        s = node["shape"]
+        weight = s["K"] * s["N"] * 2
+        return (k - 1) * weight / self.bw * 1e6 if weight > self.l2 else 0.0
 
     def split_tax(self, node, strategy, k):
-        """Extra time of k tiles over the unsplit op, plus one cross-stream
-        sync per tile (planner2.py:125-159)."""
+        """Extra time of k tiles over the unsplit op: the measured curve's
+        excess over the unsplit time where there is one, else a launch per
+        tile (plus the weight re-reads of a row split, or the output
+        re-assembly of a column split); always one cross-stream sync per
+        tile."""
         if k <= 1:
             return 0.0
-        ck = (shape_key(node), strategy, k)
-        if ck in self._tax:
-            return self._tax[ck]
-        sync = k * self.event
-        case = self.curves.get(shape_key(node))
-        if case and case.get("fit"):
-            fit = case["fit"]
-            val = max(0.0, float(fit["slope_us_per_tile"]) * (k - 1)
-                      + float(fit["intercept_us"]) - float(case["base_best_us"])
-                      ) + sync
+        memo = (shape_key(node), strategy, k)
+        if memo in self._taxes:
+            return self._taxes[memo]
+        curve = self.curves.get(shape_key(node))
+        if curve and curve.get("fit"):
+            fit = curve["fit"]
+            work = max(0.0, float(fit["slope_us_per_tile"]) * (k - 1) + float(fit["intercept_us"])
+                       - float(curve["base_best_us"]))
         elif strategy == "head":
-            val = k * self.launch + sync
+            work = k * self.launch
         elif strategy in ("col", "m2d"):
             s = node["shape"]
-            c_mb = s["M"] * s["N"] * 2 / (1024.0 * 1024.0)
-            val = k * self.launch + c_mb * 1.6 + sync
+            work = k * self.launch + _COLUMN_SPLIT_US_PER_MB * s["M"] * s["N"] * 2 / (1024.0 * 1024.0)
         else:
-            reread = 0.0
-            if node["op"] == "matmul":
-                s = node["shape"]
-                b_bytes = s["K"] * s["N"] * 2
-                if b_bytes > self.l2:
-                    reread = (k - 1) * b_bytes / self.bw * 1e6
-            val = k * self.launch + reread + sync
-        self._tax[ck] = val
-        return val
+            work = k * self.launch + self._weight_reread_us(node, k)
+        self._taxes[memo] = work + k * self.event
+        return self._taxes[memo]
 
     def split_total(self, node, strategy, k):
         return self.base(node) + self.split_tax(node, strategy, k)
@@ -299,46 +313,50 @@ def default_costs():
 # ---------------------------------------------------------- schedule ----
 
 def topo_rounds(nodes, edges):
-    """Kahn levels: round r holds the nodes whose last predecessor is in
-    round r-1, in node order (planner2.py:172-193).  Raises on a cycle."""
-    names = [n["name"] for n in nodes]
-    index = {n: i for i, n in enumerate(names)}
-    indeg = {n: 0 for n in names}
-    succ = defaultdict(list)
+    """Dependency levels: level r holds the nodes whose last producer is on
+    level r-1, each level in node order. Raises on a cycle."""
+    position = {n["name"]: i for i, n in enumerate(nodes)}
+    producers_left = {n["name"]: 0 for n in nodes}
+    consumers = defaultdict(list)
     for e in edges:
-        indeg[e["dst"]] += 1
-        succ[e["src"]].append(e["dst"])
-    frontier = [n for n in names if indeg[n] == 0]
-    rounds, node_round, seen = [], {}, 0
-    while frontier:
-        for n in frontier:
-            node_round[n] = len(rounds)
-        rounds.append(frontier)
-        seen += len(frontier)
-        nxt = set()
-        for n in frontier:
-            for v in succ[n]:
-                indeg[v] -= 1
-                if indeg[v] == 0:
-                    nxt.add(v)
-        frontier = sorted(nxt, key=index.__getitem__)
-    if seen < len(names):
+        producers_left[e["dst"]] += 1
+        consumers[e["src"]].append(e["dst"])
+    level = [n["name"] for n in nodes if producers_left[n["name"]] == 0]
+    rounds, node_round = [], {}
+    while level:
+        for name in level:
+            node_round[name] = len(rounds)
+        rounds.append(level)
+        unlocked = set()
+        for name in level:
+            for c in consumers[name]:
+                producers_left[c] -= 1
+                if producers_left[c] == 0:
+                    unlocked.add(c)
+        level = sorted(unlocked, key=position.__getitem__)
+    if len(node_round) < len(nodes):
         raise ValueError("graph cycle")
     return rounds, node_round
 
 
+# engines a task occupies: attention ("aicore") holds both the matrix and the
+# vector engine
+_HOLDS = {"aicore": ("aic", "aiv")}
+
+
 def _resources(engine):
-    return ("aic", "aiv") if engine == "aicore" else (engine,)
+    return _HOLDS.get(engine, (engine,))
 
 
 def row_ranges(total, k):
-    """k proportional row ranges; boundaries use Python's round (half to
-    even), as the reference does (planner2.py:208-210)."""
-    b = [round(i * total / k) for i in range(k + 1)]
-    return [(b[i], b[i + 1]) for i in range(k)]
+    """k proportional row ranges; the boundaries round half to even (Python's
+    round, as the reference's planner2.py:208-210)."""
+    cuts = [round(i * total / k) for i in range(k + 1)]
+    return list(zip(cuts[:-1], cuts[1:]))
 
 
-def _overlaps(src_ranges, dst_ranges):
+def _meeting(src_ranges, dst_ranges):
+    """Consumer range j -> the producer ranges it meets."""
     return {j: [i for i, (c, d) in enumerate(src_ranges) if max(a, c) < min(b, d)]
             for j, (a, b) in enumerate(dst_ranges)}
 
@@ -353,172 +371,180 @@ def _split_extent(node, strategy):
 
 
 def tile_overlap(src, dst, sp_src, sp_dst):
-    """Consumer tile -> producer tiles it reads (planner2.py:213-266).
+    """Consumer tile -> the producer tiles it reads.
 
-    A consumer reading fewer rows than the producer writes (a partial
-    collective) maps onto the head of the producer's range; equal k maps
-    one to one; different strategies depend on every tile.
-    """
+    Four cases, in this order (the reference's mapping, planner2.py:213-266):
+    a row-split consumer that reads fewer rows than the producer writes (a
+    partial collective) meets the head of the producer's range; equal k maps
+    tile to tile; splits along different axes need every producer tile;
+    otherwise the proportional row ranges decide."""
     ks, kd = sp_src["k"], sp_dst["k"]
-    dst_rows = dst["shape"].get("rows") or dst["shape"].get("M") or 0
-    src_rows = src["shape"].get("M") or src["shape"].get("rows") or 0
-    if dst_rows and src_rows and dst_rows < src_rows and sp_dst["strategy"] == "row":
-        total = _split_extent(src, sp_src["strategy"]) or src_rows
-        return _overlaps(row_ranges(total, ks),
-                         row_ranges(min(total, dst_rows), kd))
+    read = dst["shape"].get("rows") or dst["shape"].get("M") or 0
+    written = src["shape"].get("M") or src["shape"].get("rows") or 0
+    if read and written and read < written and sp_dst["strategy"] == "row":
+        extent = _split_extent(src, sp_src["strategy"]) or written
+        return _meeting(row_ranges(extent, ks), row_ranges(min(extent, read), kd))
     if ks == kd:
         return {j: [j] for j in range(kd)}
+    every = {j: list(range(ks)) for j in range(kd)}
     if sp_src["strategy"] != sp_dst["strategy"]:
-        return {j: list(range(ks)) for j in range(kd)}
-    total = _split_extent(src, sp_src["strategy"])
-    if not total:
-        return {j: list(range(ks)) for j in range(kd)}
-    return _overlaps(row_ranges(total, ks), row_ranges(total, kd))
+        return every
+    extent = _split_extent(src, sp_src["strategy"])
+    return _meeting(row_ranges(extent, ks), row_ranges(extent, kd)) if extent else every
 
 
-def simulate(graph, costs, splits=None, topo=None):
-    """List-schedule the DAG (planner2.py:269-382).
+class _Task:
+    """One tile of a node on its engine."""
+    __slots__ = ("name", "node", "tile", "parts", "dur", "strategy", "engine", "round", "order", "deps",
+                 "data_preds", "ready", "start", "end", "free_at")
 
-    A split node becomes k consecutive tasks on its engine; tile i of a
-    consumer waits for the producer tiles ``tile_overlap`` names.  Of all
-    tasks whose deps are done, the one that can start earliest runs next,
-    ties broken by (topological round, tile, node order).
-    """
-    splits = splits or {}
-    nodes = graph["nodes"]
-    by_name = {n["name"]: n for n in nodes}
-    if topo is None:
-        rounds, node_round = topo_rounds(nodes, graph["edges"])
-        order = {n["name"]: i for i, n in enumerate(nodes)}
-    else:
-        rounds, node_round, order = topo
+    def __init__(self, name, node, tile, parts, dur, strategy, rnd, order):
+        self.name, self.node, self.tile, self.parts = name, node, tile, parts
+        self.dur, self.strategy, self.engine = dur, strategy, node["engine"]
+        self.round, self.order = rnd, order
+        self.deps, self.data_preds = set(), []
+        self.ready = self.start = self.end = self.free_at = 0.0
 
-    tasks, parts_of = {}, {}
+
+def _expand(nodes, costs, splits, node_round, order):
+    """Node -> its tile tasks, each tile after the previous one."""
+    parts = {}
     for n in nodes:
         name = n["name"]
         sp = splits.get(name)
         k = int(sp.get("k", 1)) if sp else 1
         if k <= 1:
-            parts = [{"name": name, "tile": 0, "parts": 1,
-                      "dur": costs.base(n), "strategy": "none"}]
+            tiles = [_Task(name, n, 0, 1, costs.base(n), "none", node_round[name], order[name])]
         else:
             strategy = sp.get("strategy", "row")
-            dur = costs.split_total(n, strategy, k) / k
-            parts = [{"name": "%s#%d" % (name, i), "tile": i, "parts": k,
-                      "dur": dur, "strategy": strategy} for i in range(k)]
-        for i, p in enumerate(parts):
-            p.update(node=n, engine=n["engine"], round=node_round[name],
-                     order=order[name], deps=set(), data_preds=[])
-            if i:
-                p["deps"].add(parts[i - 1]["name"])
-            tasks[p["name"]] = p
-        parts_of[name] = parts
+            each = costs.split_total(n, strategy, k) / k
+            tiles = [_Task("%s#%d" % (name, i), n, i, k, each, strategy, node_round[name], order[name])
+                     for i in range(k)]
+        for prev, t in zip(tiles, tiles[1:]):
+            t.deps.add(prev.name)
+        parts[name] = tiles
+    return parts
 
-    def link(dst_part, src_part):
-        dst_part["deps"].add(src_part["name"])
-        dst_part["data_preds"].append(src_part["name"])
 
+def _wire(graph, splits, parts):
+    """Data edges between tiles: which producer tiles each consumer tile
+    reads (an unsplit side reads or feeds every tile)."""
+    by_name = {n["name"]: n for n in graph["nodes"]}
     for e in graph["edges"]:
-        src, dst = e["src"], e["dst"]
-        sp_s, sp_d = splits.get(src), splits.get(dst)
+        sp_s, sp_d = splits.get(e["src"]), splits.get(e["dst"])
         ks = int(sp_s.get("k", 1)) if sp_s else 1
         kd = int(sp_d.get("k", 1)) if sp_d else 1
-        s_parts, d_parts = parts_of[src], parts_of[dst]
+        src_tiles, dst_tiles = parts[e["src"]], parts[e["dst"]]
         if ks <= 1:
-            for dp in d_parts:
-                link(dp, s_parts[0])
-        elif kd <= 1:
-            whole = {"strategy": sp_s.get("strategy", "row"), "k": 1}
-            need = tile_overlap(by_name[src], by_name[dst], sp_s, whole)
-            for i in need.get(0, range(ks)):
-                link(d_parts[0], s_parts[i])
+            need = {j: [0] for j in range(len(dst_tiles))}
         else:
-            need = tile_overlap(by_name[src], by_name[dst], sp_s, sp_d)
-            for j, dp in enumerate(d_parts):
-                for i in need.get(j, range(ks)):
-                    link(dp, s_parts[i])
+            consumer = sp_d if kd > 1 else {"strategy": sp_s.get("strategy", "row"), "k": 1}
+            need = tile_overlap(by_name[e["src"]], by_name[e["dst"]], sp_s, consumer)
+        for j, t in enumerate(dst_tiles):
+            for i in need.get(j, range(ks)):
+                t.deps.add(src_tiles[i].name)
+                t.data_preds.append(src_tiles[i].name)
 
-    waiting = {name: len(t["deps"]) for name, t in tasks.items()}
-    succ = defaultdict(list)
-    for name, t in tasks.items():
-        for d in t["deps"]:
-            succ[d].append(name)
-    finish, engine_free = {}, defaultdict(float)
 
-    def key_of(t, dfin):
-        st = max(max(engine_free[r] for r in _resources(t["engine"])), dfin)
-        return (st, t["round"], t["tile"], t["order"])
+def _list_schedule(tasks):
+    """Run the tasks on their engines: of the tasks whose dependencies are
+    done, the one that can start earliest goes next, ties broken by
+    (dependency level, tile, node order). A heap holds the ready tasks keyed
+    by their start as of the push; engine free times only grow, so a popped
+    key that is out of date is re-keyed and pushed back, and the first key
+    found current is the minimum."""
+    free = defaultdict(float)
+    pending = {t.name: len(t.deps) for t in tasks.values()}
+    consumers = defaultdict(list)
+    for t in tasks.values():
+        for d in t.deps:
+            consumers[d].append(t.name)
 
-    ready_fin, heap = {}, []
-    for name, t in tasks.items():
-        if waiting[name] == 0:
-            ready_fin[name] = 0.0
-            heapq.heappush(heap, (key_of(t, 0.0), name))
-    schedule = []
+    def key(t):
+        return (max(max(free[r] for r in _resources(t.engine)), t.ready), t.round, t.tile, t.order)
+
+    heap = [(key(t), t.name) for t in tasks.values() if pending[t.name] == 0]
+    heapq.heapify(heap)
+    done = []
     while heap:
-        key, name = heapq.heappop(heap)
+        k, name = heapq.heappop(heap)
         t = tasks[name]
-        dfin = ready_fin[name]
-        cur = key_of(t, dfin)
-        if cur != key:
-            heapq.heappush(heap, (cur, name))
+        now = key(t)
+        if now != k:
+            heapq.heappush(heap, (now, name))
             continue
-        st = cur[0]
-        efree = max(engine_free[r] for r in _resources(t["engine"]))
-        en = st + t["dur"]
-        finish[name] = en
-        for r in _resources(t["engine"]):
-            engine_free[r] = en
-        critical = None
-        if t["data_preds"]:
-            critical = max(((d, finish[d]) for d in set(t["data_preds"])),
-                           key=lambda x: x[1])
-        schedule.append({
-            "name": name, "node": t["node"]["name"], "tile": t["tile"],
-            "parts": t["parts"], "engine": t["engine"], "round": t["round"],
-            "start": st, "end": en, "dur": t["dur"], "ready": dfin,
-            "engine_free": efree,
-            "critical": critical[0] if critical else None,
-            "critical_end": critical[1] if critical else 0.0,
-            "deps": sorted(t["deps"]),
-            "data_preds": sorted(set(t["data_preds"])),
-        })
-        for v in succ[name]:
-            waiting[v] -= 1
-            if waiting[v] == 0:
-                ready_fin[v] = max(finish[d] for d in tasks[v]["deps"])
-                heapq.heappush(heap, (key_of(tasks[v], ready_fin[v]), v))
-    if len(finish) < len(tasks):
-        missing = [n for n in tasks if n not in finish]
-        raise ValueError("task graph cycle at %s" % missing[:5])
-    schedule.sort(key=lambda x: (x["start"], x["engine"], x["name"]))
-    makespan = max((s["end"] for s in schedule), default=0.0)
-    return {"makespan_us": makespan, "tasks": schedule,
+        t.free_at = max(free[r] for r in _resources(t.engine))
+        t.start, t.end = now[0], now[0] + t.dur
+        for r in _resources(t.engine):
+            free[r] = t.end
+        done.append(t)
+        for c in consumers[name]:
+            pending[c] -= 1
+            if pending[c] == 0:
+                nxt = tasks[c]
+                nxt.ready = max(tasks[d].end for d in nxt.deps)
+                heapq.heappush(heap, (key(nxt), c))
+    if len(done) < len(tasks):
+        raise ValueError("task graph cycle at %s" % [n for n in tasks if pending[n]][:5])
+    return done
+
+
+def _record(t, tasks):
+    """The schedule entry of a placed task; `critical` is the data producer
+    that finished last (the first listed of equal ones)."""
+    critical, critical_end = None, 0.0
+    for d in dict.fromkeys(t.data_preds):
+        if critical is None or tasks[d].end > critical_end:
+            critical, critical_end = d, tasks[d].end
+    return {"name": t.name, "node": t.node["name"], "tile": t.tile, "parts": t.parts, "engine": t.engine,
+            "round": t.round, "start": t.start, "end": t.end, "dur": t.dur, "ready": t.ready,
+            "engine_free": t.free_at, "critical": critical, "critical_end": critical_end,
+            "deps": sorted(t.deps), "data_preds": sorted(set(t.data_preds))}
+
+
+def simulate(graph, costs, splits=None, topo=None):
+    """List-schedule the DAG with the given splits (the reference's
+    simulator, planner2.py:269-382, as an event loop over a heap).
+
+    A split node becomes k consecutive tile tasks on its engine; a consumer
+    tile waits for the producer tiles ``tile_overlap`` names. Returns the
+    makespan, every task's placement (sorted by start, engine, name) and the
+    dependency levels."""
+    splits = splits or {}
+    nodes = graph["nodes"]
+    if topo is None:
+        rounds, node_round = topo_rounds(nodes, graph["edges"])
+        order = {n["name"]: i for i, n in enumerate(nodes)}
+    else:
+        rounds, node_round, order = topo
+    parts = _expand(nodes, costs, splits, node_round, order)
+    _wire(graph, splits, parts)
+    tasks = {t.name: t for tiles in parts.values() for t in tiles}
+    placed = _list_schedule(tasks)
+    schedule = sorted((_record(t, tasks) for t in placed), key=lambda x: (x["start"], x["engine"], x["name"]))
+    return {"makespan_us": max((x["end"] for x in schedule), default=0.0), "tasks": schedule,
             "splits": copy.deepcopy(splits), "rounds": rounds}
 
 
 def bubbles(sched):
-    """Engine idle gaps caused by a data dependency, largest first
-    (planner2.py:385-409)."""
-    out = []
-    per_engine = defaultdict(list)
+    """Idle time an engine spent waiting for a data producer, one entry per
+    task that found its engine free before its inputs were ready; largest
+    wait first (engines in order of first appearance, then start time)."""
+    lanes = defaultdict(list)
     for t in sched["tasks"]:
-        per_engine[t["engine"]].append(t)
-    for engine, ts in per_engine.items():
-        prev_end = 0.0
-        for t in sorted(ts, key=lambda x: x["start"]):
-            gap = t["ready"] - t["engine_free"]
-            if gap > 1e-6 and t["critical"]:
-                out.append({"engine": engine, "task": t["name"],
-                            "node": t["node"], "tile": t["tile"],
-                            "round": t["round"], "dep_gap_us": gap,
-                            "engine_gap_us": t["start"] - prev_end,
-                            "critical": t["critical"],
-                            "critical_end": t["critical_end"],
-                            "start": t["start"]})
-            prev_end = max(prev_end, t["end"])
-    out.sort(key=lambda x: -x["dep_gap_us"])
-    return out
+        lanes[t["engine"]].append(t)
+    found = []
+    for engine, lane in lanes.items():
+        busy_until = 0.0
+        for t in sorted(lane, key=lambda x: x["start"]):
+            wait = t["ready"] - t["engine_free"]
+            if wait > 1e-6 and t["critical"]:
+                found.append({"engine": engine, "task": t["name"], "node": t["node"], "tile": t["tile"],
+                              "round": t["round"], "dep_gap_us": wait, "engine_gap_us": t["start"] - busy_until,
+                              "critical": t["critical"], "critical_end": t["critical_end"], "start": t["start"]})
+            busy_until = max(busy_until, t["end"])
+    found.sort(key=lambda b: -b["dep_gap_us"])
+    return found
 
 
 SUPPORTED_OPS = frozenset({"matmul", "attention", "embedding",
@@ -607,43 +633,42 @@ class _Graph:
         return self.node[_base_name(src)]["engine"] != self.node[_base_name(dst)]["engine"]
 
     def chain_after(self, start, limit=3):
-        """Same-engine single-successor chain of element-wise ops or GEMMs
-        following ``start`` (planner2.py:420-436)."""
-        engine = self.node[start]["engine"]
-        chain, cur = [], start
+        """Up to `limit` nodes that follow `start` one by one on its engine
+        (each the only same-engine consumer of the previous), element-wise
+        ops or GEMMs only."""
+        engine, chain, cur = self.node[start]["engine"], [], start
         while len(chain) < limit:
-            nxt = [v for v in self.succ.get(cur, []) if self.node[v]["engine"] == engine]
-            if len(nxt) != 1:
+            same = [v for v in self.succ.get(cur, []) if self.node[v]["engine"] == engine]
+            if len(same) != 1 or not (self.node[same[0]]["op"] in ELEMENTWISE or self.node[same[0]]["op"] == "matmul"):
                 break
-            v = nxt[0]
-            if self.node[v]["op"] not in ELEMENTWISE and self.node[v]["op"] != "matmul":
-                break
-            chain.append(v)
-            cur = v
+            cur = same[0]
+            chain.append(cur)
         return chain
 
     def producers(self, dst, fallback):
         return list(self.pred.get(dst, [])) or [fallback]
 
     def fanout(self, producers):
-        out = []
-        for p in producers:
-            out.extend(self.succ.get(p, []))
-        return out
+        return [c for p in producers for c in self.succ.get(p, [])]
+
+
+# tile counts the search tries (the reference's sets, planner2.py:447-459):
+# attention by heads, everything else by rows, GEMM tiles of >= 1024 rows
+_HEAD_KS = (2, 4, 7, 8, 14)
+_ROW_KS = (2, 4, 8, 16)
+_MIN_GEMM_TILE_ROWS = 1024
 
 
 def candidate_ks(node):
-    """Tile counts the search may try for a node (planner2.py:447-459)."""
+    """Tile counts the search may try for a node."""
     s = node["shape"]
     if node["op"] == "attention":
-        h = int(s.get("q_heads", 0))
-        return [k for k in (2, 4, 7, 8, 14) if h and h % k == 0]
+        heads = int(s.get("q_heads", 0))
+        return [k for k in _HEAD_KS if heads and heads % k == 0]
     rows = int(s.get("M") or s.get("rows") or 0)
-    if not rows:
-        return []
-    ks = [k for k in (2, 4, 8, 16) if rows % k == 0]
+    ks = [k for k in _ROW_KS if rows and rows % k == 0]
     if node["op"] == "matmul":
-        ks = [k for k in ks if rows // k >= 1024]
+        ks = [k for k in ks if rows // k >= _MIN_GEMM_TILE_ROWS]
     return ks
 
 
@@ -655,173 +680,177 @@ def _strategy(node):
     return None
 
 
-def _split_set(g, base_splits, src, dst, kp, kc, chain):
-    """Splits for one bubble: every producer of ``dst`` at kp; ``dst``, the
-    producers' other consumers and the optional chain at kc
-    (planner2.py:462-498).  None when a node cannot take its k."""
-    trial = copy.deepcopy(base_splits)
-    producers = g.producers(dst, src)
-    pset = set(producers)
-    names = list(dict.fromkeys(producers + [dst] + g.fanout(producers) + (chain or [])))
-    for name in names:
-        n = g.node[name]
-        if n["op"] == "custom_aicpu_scale":
-            if name in pset:
+class _Option:
+    """One way to remove a bubble: a full split set and its schedule."""
+    __slots__ = ("gain", "ks", "chain", "splits", "sched")
+
+    def __init__(self, gain, ks, chain, splits, sched):
+        self.gain, self.ks, self.chain, self.splits, self.sched = gain, ks, chain, splits, sched
+
+    @property
+    def label(self):
+        return "%d/%d" % self.ks
+
+
+class _SplitSearch:
+    """Bubble-driven search for row splits (the reference's greedy planner,
+    planner2.py:587-680, whose recorded decisions it reproduces).
+
+    Each round looks at the current schedule's dependency bubbles between
+    engines (one per distinct op/shape/gap signature, at most 8), prices up
+    to 12 split options per bubble by simulation (producer/consumer tile
+    counts, with and without the consumer's chain), and accepts the best
+    option, or the best union of two options of different bubbles when that
+    gains more. It stops when nothing gains `min_gain_us`."""
+
+    def __init__(self, graph, costs, min_gain_us, top_options):
+        self.g = _Graph(graph)
+        self.graph, self.costs = graph, costs
+        self.min_gain, self.top = min_gain_us, top_options
+        rounds, node_round = topo_rounds(graph["nodes"], graph["edges"])
+        self.topo = (rounds, node_round, {n["name"]: i for i, n in enumerate(graph["nodes"])})
+        self.tried = set()
+
+    def run(self, splits, topo=True):
+        return simulate(self.graph, self.costs, splits, topo=self.topo if topo else None)
+
+    def bubbles_to_try(self, sched):
+        seen, out = set(), []
+        for b in bubbles(sched):
+            if not self.g.cross_engine(b["critical"], b["node"]):
+                continue
+            if b["dep_gap_us"] < self.min_gain or (b["node"], b["critical"]) in self.tried:
+                continue
+            src, dst = self.g.node[_base_name(b["critical"])], self.g.node[b["node"]]
+            sig = (src["op"], dst["op"], json.dumps(src.get("shape", {}), sort_keys=True),
+                   json.dumps(dst.get("shape", {}), sort_keys=True), round(b["dep_gap_us"], 1))
+            if sig not in seen:
+                seen.add(sig)
+                out.append(b)
+        return out[:8]
+
+    def splits_for(self, base, src, dst, kp, kc, chain):
+        """Every producer of dst at kp; dst, the producers' other consumers and
+        the optional chain at kc. None when a node cannot take its k."""
+        trial = copy.deepcopy(base)
+        producers = self.g.producers(dst, src)
+        for name in dict.fromkeys(producers + [dst] + self.g.fanout(producers) + (chain or [])):
+            n = self.g.node[name]
+            if n["op"] == "custom_aicpu_scale":
+                if name in producers:
+                    return None
+                continue
+            k = kp if name in producers else kc
+            strategy = _strategy(n)
+            if strategy is None or k not in candidate_ks(n):
                 return None
-            continue
-        k = kp if name in pset else kc
-        strategy = _strategy(n)
-        if strategy is None or k not in candidate_ks(n):
-            return None
-        trial[name] = {"strategy": strategy, "k": k}
-    return trial
+            trial[name] = {"strategy": strategy, "k": k}
+        return trial
 
-
-def _bubble_options(g, costs, cur, b, min_gain_us, topo=None):
-    """Split options with positive gain for one bubble, best first
-    (planner2.py:501-546)."""
-    src, dst = _base_name(b["critical"]), b["node"]
-    if g.node[src]["engine"] == g.node[dst]["engine"]:
-        return []
-    chain = g.chain_after(dst)
-    producers = g.producers(dst, src)
-    pset = set(producers)
-    min_tax = 0.0
-    for name in dict.fromkeys(producers + [dst] + g.fanout(producers)):
-        n = g.node[name]
-        if n["op"] == "custom_aicpu_scale" and name in pset:
+    def options(self, cur, b):
+        """Options with a positive gain for bubble b, best first."""
+        src, dst = _base_name(b["critical"]), b["node"]
+        if self.g.node[src]["engine"] == self.g.node[dst]["engine"]:
             return []
-        ks = candidate_ks(n)
-        if not ks:
+        producers = self.g.producers(dst, src)
+        # the cheapest split of every node involved must cost less than the gap
+        floor = 0.0
+        for name in dict.fromkeys(producers + [dst] + self.g.fanout(producers)):
+            n = self.g.node[name]
+            ks = candidate_ks(n)
+            if not ks or (n["op"] == "custom_aicpu_scale" and name in producers):
+                return []
+            floor += self.costs.split_tax(n, "head" if n["op"] == "attention" else "row", min(ks))
+        if floor >= b["dep_gap_us"]:
             return []
-        min_tax += costs.split_tax(n, "head" if n["op"] == "attention" else "row", min(ks))
-    if min_tax >= b["dep_gap_us"]:
-        return []
-    pairs = {(kp, kc) for kp in candidate_ks(g.node[src])
-             for kc in candidate_ks(g.node[dst])}
-    pairs = sorted(pairs, key=lambda x: (x[0] > x[1], x[0], x[1]))[:6]
-    options = []
-    for kp, kc in pairs:
-        for with_chain in (False, True):
-            trial = _split_set(g, cur["splits"], src, dst, kp, kc,
-                               chain if with_chain else None)
-            if not trial:
-                continue
-            try:
-                s2 = simulate(g.graph, costs, trial, topo=topo)
-            except (ValueError, KeyError):
-                continue
-            gain = cur["makespan_us"] - s2["makespan_us"]
-            if gain >= min_gain_us:
-                options.append((gain, (kp, kc), with_chain, trial, s2))
-    options.sort(key=lambda x: -x[0])
-    return options
+        chain = self.g.chain_after(dst)
+        pairs = sorted({(kp, kc) for kp in candidate_ks(self.g.node[src]) for kc in candidate_ks(self.g.node[dst])},
+                       key=lambda x: (x[0] > x[1], x[0], x[1]))[:6]
+        found = []
+        for kp, kc in pairs:
+            for with_chain in (False, True):
+                trial = self.splits_for(cur["splits"], src, dst, kp, kc, chain if with_chain else None)
+                if not trial:
+                    continue
+                try:
+                    sched = self.run(trial)
+                except (ValueError, KeyError):
+                    continue
+                gain = cur["makespan_us"] - sched["makespan_us"]
+                if gain >= self.min_gain:
+                    found.append(_Option(gain, (kp, kc), with_chain, trial, sched))
+        found.sort(key=lambda o: -o.gain)
+        return found
+
+    def best_move(self, cur, per_bubble):
+        """The best single option, or a better union of two options of
+        different bubbles. Returns ([(bubble, option)...], gain, splits, sched)."""
+        shortlist = [(b, o) for b, opts in per_bubble for o in opts[:self.top]]
+        b0, o0 = max(shortlist, key=lambda bo: bo[1].gain)  # first of equal gains
+        best = ([(b0, o0)], o0.gain, o0.splits, o0.sched)
+        ranked = sorted(shortlist, key=lambda bo: -bo[1].gain)[:8]
+        for i, (b1, o1) in enumerate(ranked):
+            for b2, o2 in ranked[i + 1:]:
+                if (b1["node"], b1["critical"]) == (b2["node"], b2["critical"]):
+                    continue
+                merged = _merge_splits(o1.splits, o2.splits)
+                if merged is None:
+                    continue
+                try:
+                    sched = self.run(merged, topo=False)
+                except (ValueError, KeyError):
+                    continue
+                gain = cur["makespan_us"] - sched["makespan_us"]
+                if gain > best[1] + 1e-9:
+                    best = ([(b1, o1), (b2, o2)], gain, merged, sched)
+        return best
 
 
-def _union(t1, t2):
-    """Merge two split sets; None when they disagree on a node."""
-    trial = copy.deepcopy(t1)
-    for name, spec in t2.items():
-        if name in trial and trial[name] != spec:
+def _merge_splits(a, b):
+    """Union of two split sets; None when they give a node different splits."""
+    out = copy.deepcopy(a)
+    for name, spec in b.items():
+        if out.setdefault(name, dict(spec)) != spec:
             return None
-        trial[name] = dict(spec)
-    return trial
+    return out
 
 
-def _decision(rnd, b, options, accepted):
-    best = options[0] if options else None
+def _decision_record(rnd, b, options, accepted):
+    top = options[0] if options else None
     return {"round": rnd, "consumer": b["node"], "engine": b["engine"],
-            "critical_edge": "%s -> %s" % (b["critical"], b["node"]),
-            "dep_gap_us": b["dep_gap_us"],
-            "k": ("%d/%d" % best[1]) if best else None,
-            "split_consumer_chain": best[2] if best else False,
-            "predicted_gain_us": best[0] if best else 0.0,
-            "alternatives": [{"k": "%d/%d" % o[1], "gain_us": o[0],
-                              "split_chain": o[2]} for o in options],
+            "critical_edge": "%s -> %s" % (b["critical"], b["node"]), "dep_gap_us": b["dep_gap_us"],
+            "k": top.label if top else None, "split_consumer_chain": top.chain if top else False,
+            "predicted_gain_us": top.gain if top else 0.0,
+            "alternatives": [{"k": o.label, "gain_us": o.gain, "split_chain": o.chain} for o in options],
             "accepted": accepted}
 
 
 def greedy_plan(graph, costs, max_rounds=40, min_gain_us=1.0, top_options=3):
-    """Bubble-driven split search (planner2.py:587-680).
+    """Bubble-driven split search (see _SplitSearch).
 
-    Each round: take the cross-engine dependency bubbles of the current
-    schedule (one per distinct (op, shape, gap) signature, at most 8), price
-    up to 12 split options per bubble by simulation, then accept the best
-    single option or the best union of two options from different bubbles.
-    Stops when no option gains ``min_gain_us``.
-
-    Returns (splits, schedule, history, base_makespan_us, decisions).
-    """
-    g = _Graph(graph)
-    nodes = graph["nodes"]
-    rounds, node_round = topo_rounds(nodes, graph["edges"])
-    topo = (rounds, node_round, {n["name"]: i for i, n in enumerate(nodes)})
+    Returns (splits, schedule, history, base_makespan_us, decisions)."""
+    search = _SplitSearch(graph, costs, min_gain_us, top_options)
     splits = {}
-    cur = simulate(graph, costs, splits, topo=topo)
+    cur = search.run(splits)
     base = cur["makespan_us"]
-    history, decisions, tried = [], [], set()
+    history, decisions = [], []
     for rnd in range(max_rounds):
-        cands, sigs = [], set()
-        for b in bubbles(cur):
-            if not g.cross_engine(b["critical"], b["node"]):
-                continue
-            if b["dep_gap_us"] < min_gain_us or (b["node"], b["critical"]) in tried:
-                continue
-            src, dst = g.node[_base_name(b["critical"])], g.node[b["node"]]
-            sig = (src["op"], dst["op"],
-                   json.dumps(src.get("shape", {}), sort_keys=True),
-                   json.dumps(dst.get("shape", {}), sort_keys=True),
-                   round(b["dep_gap_us"], 1))
-            if sig not in sigs:
-                sigs.add(sig)
-                cands.append(b)
-        if not cands:
-            break
-        per_bubble = []
-        for b in cands[:8]:
-            opts = _bubble_options(g, costs, cur, b, min_gain_us, topo=topo)
-            if opts:
-                per_bubble.append((b, opts))
+        cands = search.bubbles_to_try(cur)
+        per_bubble = [(b, opts) for b, opts in ((b, search.options(cur, b)) for b in cands) if opts]
         if not per_bubble:
             break
-        best = None
-        for b, opts in per_bubble:
-            for o in opts[:top_options]:
-                if best is None or o[0] > best[1]:
-                    best = ([(b, o)], o[0], o[3], o[4])
-        flat = sorted(((b, o) for b, opts in per_bubble for o in opts[:top_options]),
-                      key=lambda x: -x[1][0])[:8]
-        for i, (b1, o1) in enumerate(flat):
-            for b2, o2 in flat[i + 1:]:
-                if b1["node"] == b2["node"] and b1["critical"] == b2["critical"]:
-                    continue
-                trial = _union(o1[3], o2[3])
-                if trial is None:
-                    continue
-                try:
-                    s2 = simulate(graph, costs, trial)
-                except (ValueError, KeyError):
-                    continue
-                gain = cur["makespan_us"] - s2["makespan_us"]
-                if gain > best[1] + 1e-9:
-                    best = ([(b1, o1), (b2, o2)], gain, trial, s2)
-        chosen, gain, trial, s2 = best
-        chosen_ids = {id(b) for b, _ in chosen}
-        for b, opts in per_bubble:
-            decisions.append(_decision(rnd, b, opts, id(b) in chosen_ids))
-        labels = []
+        chosen, gain, trial, sched = search.best_move(cur, per_bubble)
+        picked = {id(b) for b, _ in chosen}
+        decisions += [_decision_record(rnd, b, opts, id(b) in picked) for b, opts in per_bubble]
         for b, o in chosen:
-            labels.append("k=%d/%d" % o[1] + ("+chain" if o[2] else ""))
-            for name in o[3]:
-                tried.add((name, b["critical"]))
-        history.append({"round": rnd, "gain_us": gain, "k": ", ".join(labels),
-                        "split_chain": any(o[2] for _, o in chosen),
-                        "splits": copy.deepcopy(trial),
+            search.tried.update((name, b["critical"]) for name in o.splits)
+        history.append({"round": rnd, "gain_us": gain,
+                        "k": ", ".join("k=" + o.label + ("+chain" if o.chain else "") for _, o in chosen),
+                        "split_chain": any(o.chain for _, o in chosen), "splits": copy.deepcopy(trial),
                         "bubble": chosen[0][0],
-                        "bubbles": [{"consumer": b["node"], "critical": b["critical"]}
-                                    for b, _ in chosen],
-                        "makespan_us": s2["makespan_us"]})
-        splits, cur = trial, s2
+                        "bubbles": [{"consumer": b["node"], "critical": b["critical"]} for b, _ in chosen],
+                        "makespan_us": sched["makespan_us"]})
+        splits, cur = trial, sched
     return splits, cur, history, base, decisions
 
 
