@@ -149,6 +149,20 @@ int kr_op_gemm_streamk(int dtype, const void *A, int64_t lda, const void *Bt, in
                        const void *bias, int M, int N, int K, void *ws, size_t ws_bytes, int32_t *counters,
                        int n_counters, void *stream);
 
+/* kr_op_gemm_streamk without a workspace argument, allocating nothing: the
+ * partial sums and tile counters live in a device array of the library
+ * (48 MiB of partials, 1024 counters; each GPU it runs on holds one until
+ * the process ends). No counterpart in the reference: for callers that
+ * cannot allocate device memory (code under HIP graph capture, serving loops
+ * that forbid hipMalloc). Same plan, piece order and bits as
+ * kr_op_gemm_streamk; the counters are cleared at every call. Shapes whose
+ * split needs more than the array holds fail with an error naming both
+ * sizes. All calls on one GPU share the array: calls that may overlap in
+ * time on one GPU (different streams, or hosts threads without ordering)
+ * race and must not be issued. */
+int kr_op_gemm_streamk_noalloc(int dtype, const void *A, int64_t lda, const void *Bt, int64_t ldb, void *C,
+                               int64_t ldc, const void *bias, int M, int N, int K, void *stream);
+
 /* Elementwise op on [rows, cols]; x1 used by mul/add/swiglu; dtype_out
  * differs from dtype_in only for cast. tile_rows = relay granularity
  * (0 = rows); grid = workgroups (0 = sized to the tensor). wait/pub may be

@@ -1,6 +1,7 @@
 // C ABI of the op-level kernels (include/kr_ops.h).
 #include "../../include/kr_ops.h"
 
+#include <mutex>
 #include <string>
 #include <vector>
 
@@ -61,6 +62,47 @@ kr::RelayPub ToPub(const kr_pub *p)
 }
 
 hipStream_t S(void *s) { return static_cast<hipStream_t>(s); }
+
+// ------------------------------------------------ allocation-free stream-K
+// kr_op_gemm_streamk_noalloc keeps the stream-K partial sums and tile
+// counters in this file-scope device array instead of a caller workspace:
+// 48 MiB of fp32 partials (a split of up to 48 pieces of 256x256 tiles, e.g.
+// the Qwen2.5-0.5B down projection 2048x896x4864: 32 MiB) and 1024 tile
+// counters. Every GPU the library runs on holds its own copy until the
+// process ends. In host code `scratch` names a host-side stand-in, never the
+// device memory: its device address comes from hipGetSymbolAddress, once per
+// device with that device current, and only that address reaches kernels.
+constexpr size_t kScratchPartialBytes = size_t(48) << 20;
+constexpr int kScratchCounters = 1024;
+static __device__ __align__(256) unsigned char scratch[kScratchPartialBytes + kScratchCounters * 4];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void *g_scratch[kMaxDevices] = {};
+
+// Device address of this device's scratch array (set up on the first call
+// on the device, with the device current).
+unsigned char *ScratchOnCurrentDevice()
+{
+    int dev = 0;
+    kr::Check(hipGetDevice(&dev), "hipGetDevice");
+    if (dev < 0 || dev >= kMaxDevices) throw std::runtime_error("noalloc: device id out of range");
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (g_scratch[dev] == nullptr) {
+        void *p = nullptr;
+        kr::Check(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)), "hipGetSymbolAddress(scratch)");
+        g_scratch[dev] = p;
+    }
+    return static_cast<unsigned char *>(g_scratch[dev]);
+}
+
+// The counters start every call at zero (a fill kernel, not a memset, so the
+// call also works under graph capture).
+__global__ void ZeroCountersKernel(int32_t *c, int n)
+{
+    const int i = int(blockIdx.x * blockDim.x + threadIdx.x);
+    if (i < n) c[i] = 0;
+}
 
 }  // namespace
 
@@ -183,6 +225,47 @@ int kr_op_gemm_streamk(int dtype, const void *A, int64_t lda, const void *Bt, in
         d.sk_ws_bytes = ws_bytes;
         d.sk_cnt = counters;
         d.sk_cnt_len = n_counters;
+        kr::GemmLaunch(d, S(stream));
+    });
+}
+
+int kr_op_gemm_streamk_noalloc(int dtype, const void *A, int64_t lda, const void *Bt, int64_t ldb, void *C,
+                               int64_t ldc, const void *bias, int M, int N, int K, void *stream)
+{
+    return Guard([&] {
+        size_t ws_bytes = 0;
+        int counters = 0;
+        kr::GemmStreamKNeeds(M, N, K, &ws_bytes, &counters);
+        if (ws_bytes > kScratchPartialBytes || counters > kScratchCounters)
+            throw std::runtime_error("gemm_streamk_noalloc: this shape's split needs " + std::to_string(ws_bytes) +
+                                     " bytes of partials and " + std::to_string(counters) +
+                                     " counters; the library's scratch holds " +
+                                     std::to_string(kScratchPartialBytes) + " bytes and " +
+                                     std::to_string(kScratchCounters) + " counters (use kr_op_gemm_streamk)");
+        kr::GemmDesc d;
+        d.dtype = dtype;
+        d.A = A;
+        d.Bt = Bt;
+        d.C = C;
+        d.bias = bias;
+        d.lda = lda;
+        d.ldb = ldb;
+        d.ldc = ldc;
+        d.M = M;
+        d.N = N;
+        d.K = K;
+        if (ws_bytes > 0) {
+            unsigned char *base = ScratchOnCurrentDevice();
+            int32_t *cnt = reinterpret_cast<int32_t *>(base + kScratchPartialBytes);
+            hipLaunchKernelGGL(ZeroCountersKernel, dim3((counters + 255) / 256), dim3(256), 0, S(stream), cnt,
+                               counters);
+            kr::Check(hipGetLastError(), "zero counters launch");
+            d.streamk = true;
+            d.sk_ws = base;
+            d.sk_ws_bytes = kScratchPartialBytes;
+            d.sk_cnt = cnt;
+            d.sk_cnt_len = kScratchCounters;
+        }
         kr::GemmLaunch(d, S(stream));
     });
 }

@@ -62,12 +62,13 @@ def _lib():
                                          i32, vp]
         L.kr_op_gemm_add_rmsnorm.argtypes = [i32, vp, i64, vp, i64, vp, i32, i32, i32, vp, vp, vp, vp, vp, f32,
                                              ctypes.POINTER(KrPub), ctypes.c_uint32, vp, ctypes.c_size_t, vp, i32, vp]
+        L.kr_op_gemm_streamk_noalloc.argtypes = [i32, vp, i64, vp, i64, vp, i64, vp, i32, i32, i32, vp]
         L.kr_op_stream_create.argtypes = []
         L.kr_op_stream_create.restype = vp
         L.kr_op_stream_destroy.argtypes = [vp]
         L.kr_op_stream_destroy.restype = ctypes.c_int
         for name in ("kr_op_gemm", "kr_op_gemm_swiglu", "kr_op_gemm_swiglu_epilogue", "kr_op_gemm_streamk",
-                     "kr_op_gemm_add_rmsnorm",
+                     "kr_op_gemm_add_rmsnorm", "kr_op_gemm_streamk_noalloc",
                      "kr_op_gemm_streamk_workspace", "kr_op_elementwise", "kr_op_rowop", "kr_op_wait", "kr_op_publish",
                      "kr_op_embedding", "kr_op_rope", "kr_op_attention", "kr_op_attention_workspace",
                      "kr_op_attention_split", "kr_op_transpose"):
@@ -186,6 +187,15 @@ def gemm_streamk(A, Bt, C, ws, counters, bias=None, stream=None):
     _check(_lib().kr_op_gemm_streamk(_dt(A), _ptr(A), A.stride(0), _ptr(Bt), Bt.stride(0), _ptr(C), C.stride(0),
                                      _ptr(bias), M, N, K, _ptr(ws), ws.numel() * ws.element_size(),
                                      _ptr(counters), counters.numel(), _stream(stream)))
+
+
+def gemm_streamk_noalloc(A, Bt, C, bias=None, stream=None):
+    """gemm_streamk with the library's own scratch (no workspace argument,
+    nothing allocated); raises for a split larger than the scratch."""
+    M, K = A.shape
+    N = Bt.shape[0]
+    _check(_lib().kr_op_gemm_streamk_noalloc(_dt(A), _ptr(A), A.stride(0), _ptr(Bt), Bt.stride(0), _ptr(C),
+                                             C.stride(0), _ptr(bias), M, N, K, _stream(stream)))
 
 
 def gemm_swiglu_epilogue(A, Bt, act, stream=None):
