@@ -37,7 +37,13 @@ enum {
 };
 
 /* Row-reduction ops for kr_op_rowop. */
-enum { KR_ROW_SOFTMAX = 0, KR_ROW_RMSNORM = 1, KR_ROW_ADD_RMSNORM = 2 };
+enum {
+    KR_ROW_SOFTMAX = 0,
+    KR_ROW_RMSNORM = 1,
+    KR_ROW_ADD_RMSNORM = 2,
+    KR_ROW_LAYERNORM = 3  /* gamma = weight [cols], x1 = bias [cols] (aclnnLayerNorm,
+                             reference exec/runtime/op_impl.cpp:237-254) */
+};
 
 /* Relay control blocks: 8 x int32 each, zero-initialised once by the owner
  * (layout: published, consumed, status, arrive, done, timed_out, -, -; the

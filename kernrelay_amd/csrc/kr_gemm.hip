@@ -219,28 +219,48 @@ __device__ void TailSwiglu(const GemmParams &p)
 // The producer's own workgroups consume its released row tiles (the
 // reference's down -> Add+RMSNorm tile loop, exec/qwen_main.cpp:1274-1302,
 // without the all-reduce): a workgroup that has stored its C tile and arrived
-// on relay tile `tile`'s flag waits for the tile's release (all of its
-// producer workgroups have arrived), then computes Add+RMSNorm for rows
-// lo + worker*waves + wave, stepping by workers*waves, one row per wave at a
-// time, with the row code of the standalone row kernel. C is read at device
-// scope (written by other XCDs' workgroups of this launch). The last of the
-// tile's `workers` consumes the release (consumed + 1, status 1, or 2 when
-// any wait ran out of spins). Safe from deadlock because the launcher only
-// asks for it when a relay tile's producer workgroups fit the device at once
-// (they are dispatched in order, so they are all resident or finished).
-template <int DT, int CPL>
+// on relay tile `tile`'s flag (as the tile's `worker`-th arrival) waits for
+// the tile's release (all of its producer workgroups have arrived), then
+// computes Add+RMSNorm for rows lo + worker*waves + wave, stepping by
+// workers*waves, one row per wave, RB rows' loads in flight at a time, with
+// the row code of the standalone row kernel. C is read at device scope
+// (written by other XCDs' workgroups of this launch). The last of the tile's
+// `workers` consumes the release (consumed + 1, status 1, or 2 when any wait
+// ran out of spins). Safe from deadlock because the launcher only asks for
+// it when the workgroups a tile waits for are resident together: the whole
+// grid, or (dispatched in order, relay tile after relay tile) one relay
+// tile's producers.
+template <int DT, int CPL, int RB>
 __device__ __forceinline__ void NormRows(const GemmParams &p, int lo, int hi, int first, int step)
 {
     const int ln = threadIdx.x & 63;
-    for (int r = lo + first; r < hi; r += step) {
-        const int64_t o = int64_t(r) * p.N;
-        AddRmsNormRow<DT, CPL, true>(p.rn_res + o, p.C + o, p.rn_gamma, p.rn_y + o,
-                                     p.rn_sum != nullptr ? p.rn_sum + o : nullptr,
-                                     p.rn_rstd != nullptr ? p.rn_rstd + r : nullptr, p.N, p.rn_eps, ln, false);
+    // a wave's rows are the same for all its lanes: kept in scalar registers,
+    // the device-scope loads take their base as a plain buffer resource
+    // (a row index the compiler thinks may differ per lane would wrap every
+    // load in a loop over the lanes' distinct bases)
+    first = __builtin_amdgcn_readfirstlane(first);
+    if (lo + first >= hi) return;
+    uint4 g[CPL];
+    RowGammaLoad<CPL>(p.rn_gamma, p.N, ln, g);
+    for (int r0 = lo + first; r0 < hi; r0 += RB * step) {
+        RowIn<CPL> in[RB];
+#pragma unroll
+        for (int j = 0; j < RB; ++j) {
+            const int r = min(r0 + j * step, hi - 1);  // past the end: re-read, never used
+            AddRmsNormLoad<CPL, true>(p.rn_res + int64_t(r) * p.N, p.C + int64_t(r) * p.N, p.N, ln, in[j]);
+        }
+#pragma unroll
+        for (int j = 0; j < RB; ++j) {
+            const int r = r0 + j * step;
+            if (r >= hi) break;
+            const int64_t o = int64_t(r) * p.N;
+            AddRmsNormFinish<DT, CPL>(in[j], g, p.rn_y + o, p.rn_sum != nullptr ? p.rn_sum + o : nullptr,
+                                      p.rn_rstd != nullptr ? p.rn_rstd + r : nullptr, p.N, p.rn_eps, ln, false);
+        }
     }
 }
 
-template <int DT>
+template <int DT, int NW, int WPE>
 __device__ void NormTail(const GemmParams &p, int tile, int worker, int workers)
 {
     int32_t *flag = p.pub.ctrl + size_t(p.pub.flag0 + tile) * kWords;
@@ -248,14 +268,18 @@ __device__ void NormTail(const GemmParams &p, int tile, int worker, int workers)
     __syncthreads();
     const int R = p.pub.rows_per_tile;
     const int lo = tile * R, hi = min(lo + R, p.M);
-    const int nw = int(blockDim.x) >> 6;
-    const int first = worker * nw + int(threadIdx.x >> 6);
-    const int step = workers * nw;
+    const int first = worker * NW + int(threadIdx.x >> 6);
+    const int step = workers * NW;
+    // rows in flight per wave: what the registers hold without spilling
+    // (WPE waves per SIMD share its 512 registers; loads land in the 256
+    // architectural ones)
+    constexpr int RB4 = WPE == 2 ? 2 : 4;
+    constexpr int RB8 = WPE == 2 ? 1 : 2;
     switch (p.rn_cpl) {
-        case 1: NormRows<DT, 1>(p, lo, hi, first, step); break;
-        case 2: NormRows<DT, 2>(p, lo, hi, first, step); break;
-        case 4: NormRows<DT, 4>(p, lo, hi, first, step); break;
-        default: NormRows<DT, 8>(p, lo, hi, first, step); break;
+        case 1: NormRows<DT, 1, RB4>(p, lo, hi, first, step); break;
+        case 2: NormRows<DT, 2, RB4>(p, lo, hi, first, step); break;
+        case 4: NormRows<DT, 4, RB4>(p, lo, hi, first, step); break;
+        default: NormRows<DT, 8, RB8>(p, lo, hi, first, step); break;
     }
     __syncthreads();
     if (threadIdx.x == 0) {
@@ -557,9 +581,9 @@ GemmKernel(GemmParams p)
         StoreTile<DT, BM, BN, kThreads>(p, acc, smem, m0, n0, wm, wn, lane);
     }
     if (p.pub.ctrl != nullptr) {
-        RelayArrive(p.pub, m0 / p.pub.rows_per_tile);
-        // relay order: workgroups [t*arrivals, (t+1)*arrivals) make tile t
-        if (p.rn_y != nullptr) NormTail<DT>(p, m0 / p.pub.rows_per_tile, int(blockIdx.x) % p.pub.arrivals, p.pub.arrivals);
+        const int tile = m0 / p.pub.rows_per_tile;
+        const int a = RelayArriveIndexed(p.pub, tile, reinterpret_cast<int *>(smem));  // the tile stage is free
+        if (p.rn_y != nullptr) NormTail<DT, kThreads / 64, BM * BN >= 256 * 128 ? 1 : 2>(p, tile, a, p.pub.arrivals);
     }
     RelayFinish(p.wait);
 }
@@ -786,6 +810,10 @@ void LaunchTyped(const GemmParams &base, int order_rows, int tail_tiles, hipStre
         if (!NormRelayResident(BM, BN, p.M, p.N, p.pub.rows_per_tile, sk != nullptr ? sk->G : 0))
             throw std::runtime_error("gemm: a relay tile's producer workgroups do not fit the device at once; "
                                      "the Add+RMSNorm relay consumer would wait on workgroups not yet placed");
+        // a grid resident as a whole releases every tile at about the same
+        // time whatever the order: keep the grouped raster (square patches
+        // per XCD, less operand traffic than relay-tile order)
+        if (sk == nullptr && p.gemm_wgs <= CuCount() * (BM * BN >= 256 * 128 ? 1 : 2)) p.order_rows = 0;
     }
     if (sk != nullptr) {
         if (BM != 256 || BN != 256 || sk->tiles != p.gemm_wgs) throw std::logic_error("gemm: stream-K plan mismatch");

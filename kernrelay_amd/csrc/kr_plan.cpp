@@ -44,7 +44,7 @@ namespace plan {
 
 using json::Value;
 
-enum class Op { MatMul, Gelu, Softmax, Cast, Add, Silu, Mul, Swiglu, RmsNorm, AddRmsNorm };
+enum class Op { MatMul, Gelu, Softmax, Cast, Add, Silu, Mul, Swiglu, RmsNorm, AddRmsNorm, LayerNorm };
 
 Op ParseOp(const std::string &s)
 {
@@ -58,8 +58,9 @@ Op ParseOp(const std::string &s)
     if (s == "swiglu") return Op::Swiglu;
     if (s == "rmsnorm") return Op::RmsNorm;
     if (s == "add_rmsnorm") return Op::AddRmsNorm;
+    if (s == "layernorm") return Op::LayerNorm;
     throw std::runtime_error("op '" + s + "' is not built on this target "
-                             "(supported: matmul gelu softmax cast add silu mul swiglu rmsnorm add_rmsnorm)");
+                             "(supported: matmul gelu softmax cast add silu mul swiglu rmsnorm add_rmsnorm layernorm)");
 }
 
 int ParseDType(const std::string &s)
@@ -147,7 +148,8 @@ SchedDoc ParseSchedule(const Value &root)
         s.n = int64_t(n.Num("n"));
         s.tiles = std::max(1, int(n.Num("tiles", 1)));
         s.split = n.Flag("split", false);
-        s.eps = float(n.Num("eps", 1e-6));
+        // aclnnLayerNorm runs with eps 1e-5 in the reference (op_impl.cpp:248)
+        s.eps = float(n.Num("eps", s.op == Op::LayerNorm ? 1e-5 : 1e-6));
         if (n.Has("preds"))
             for (const auto &p : n.At("preds").Items()) s.preds.push_back(p.AsString());
         if (n.Has("inputs"))
@@ -278,7 +280,7 @@ void NormalizeTopology(SchedDoc &doc)
 
 // ------------------------------------------------------------------ runtime
 struct NodeBuf {
-    DevBuf out, bt, own_in, aux, gamma, sum;
+    DevBuf out, bt, own_in, aux, gamma, sum, beta;
     size_t out_bytes = 0;
 };
 
@@ -514,7 +516,8 @@ private:
         if (n.preds.empty()) b.own_in.Alloc(rows * InCols(n) * 2);
         if (n.op == Op::MatMul) b.bt.Alloc(size_t(n.k) * n.n * 2);
         if (IsBinary(n.op) && n.preds.size() < 2) b.aux.Alloc(rows * cols * 2);
-        if (n.op == Op::RmsNorm || n.op == Op::AddRmsNorm) b.gamma.Alloc(cols * 2);
+        if (n.op == Op::RmsNorm || n.op == Op::AddRmsNorm || n.op == Op::LayerNorm) b.gamma.Alloc(cols * 2);
+        if (n.op == Op::LayerNorm) b.beta.Alloc(cols * 2);
         if (n.op == Op::AddRmsNorm) b.sum.Alloc(rows * cols * 2);
         rc.bufs[n.id] = std::move(b);
     }
@@ -541,6 +544,11 @@ private:
             if (b.gamma.get()) {
                 auto h = HostInput(n, "gamma", cols, seed + 2, n.dtype);
                 Check(hipMemcpy(b.gamma.get(), h.data(), h.size() * 2, hipMemcpyHostToDevice), "upload gamma");
+            }
+            if (b.beta.get()) {
+                // LayerNorm weight seed + 2, bias seed + 3 (exec_main.cpp:519-528)
+                auto h = HostInput(n, "beta", cols, seed + 3, n.dtype);
+                Check(hipMemcpy(b.beta.get(), h.data(), h.size() * 2, hipMemcpyHostToDevice), "upload beta");
             }
             if (b.aux.get()) {
                 auto h = HostInput(n, "x1", rows * cols, seed + 3, n.dtype);
@@ -968,12 +976,16 @@ private:
             }
             case Op::Softmax:
             case Op::RmsNorm:
-            case Op::AddRmsNorm: {
+            case Op::AddRmsNorm:
+            case Op::LayerNorm: {
                 RowDesc d;
-                d.op = n.op == Op::Softmax ? kRowSoftmax : (n.op == Op::RmsNorm ? kRowRmsNorm : kRowAddRmsNorm);
+                d.op = n.op == Op::Softmax     ? kRowSoftmax
+                       : n.op == Op::RmsNorm   ? kRowRmsNorm
+                       : n.op == Op::LayerNorm ? kRowLayerNorm
+                                               : kRowAddRmsNorm;
                 d.dtype = n.dtype;
                 d.x0 = in_tile;
-                d.x1 = x1;
+                d.x1 = n.op == Op::LayerNorm ? b.beta.get() : x1;
                 d.gamma = b.gamma.get();
                 d.y = out_tile;
                 d.sum_out = b.sum.get() ? static_cast<char *>(b.sum.get()) + size_t(out_off) * n.cols * 2 : nullptr;
@@ -1167,10 +1179,101 @@ int ParseDevice(const char *devices)
     return dev < 0 ? 0 : dev;
 }
 
+// Cross-stream sync micro-benchmark (the reference's NHP_SYNC_BENCH,
+// exec/exec_main.cpp:751-833): n producer/consumer kernel pairs on two
+// streams with hardware queues of their own. Every mode launches the same two
+// one-workgroup kernels per pair (a publish on the producer stream, a wait on
+// the consumer stream) and changes only the synchronisation: "nosync" (the
+// wait targets a block published beforehand, so it returns at once),
+// "event" (a hipEvent record / stream wait between them as well) and "flag"
+// (the wait spins on the block this pair's publish releases). Wall time per
+// pair, median over rounds; event/flag minus nosync is the cost of the sync.
+double SyncBenchMode(const std::string &mode, int n, int rounds, int warmup, const StreamPair &sp, DevBuf &ctrl,
+                     std::vector<hipEvent_t> &events, int *timeouts)
+{
+    std::vector<double> samples;
+    int32_t *blocks = ctrl.as<int32_t>();
+    std::vector<int32_t> ready(size_t(n) * kWords, 0);
+    for (int i = 0; i < n; ++i) ready[size_t(i) * kWords + kOffPublished] = 1 << 30;
+    for (int r = 0; r < warmup + rounds; ++r) {
+        // blocks [0, n): released by this round's publishes; [n, 2n): already released
+        Check(hipMemset(blocks, 0, size_t(n) * kWords * 4), "sync clear flags");
+        Check(hipMemcpy(blocks + size_t(n) * kWords, ready.data(), ready.size() * 4, hipMemcpyHostToDevice),
+              "sync preset flags");
+        Check(hipDeviceSynchronize(), "sync reset");
+        const auto t0 = Clock::now();
+        for (int i = 0; i < n; ++i) {
+            RelayPub pub{};
+            pub.ctrl = blocks;
+            pub.flag0 = i;
+            pub.rows_per_tile = 1;
+            PublishLaunch(pub, 0, sp.prod);
+            if (mode == "event") {
+                Check(hipEventRecord(events[i], sp.prod), "sync record");
+                Check(hipStreamWaitEvent(sp.cons, events[i], 0), "sync wait event");
+            }
+            RelayWait w{};
+            w.ctrl = blocks;
+            w.flag0 = mode == "flag" ? i : n + i;
+            w.state0 = i;
+            w.prod_rows = 1;
+            w.adv_lo = 0;
+            w.adv_hi = 1;
+            w.max_spins = kDefaultMaxSpins;
+            WaitLaunch(w, 0, 1, sp.cons);
+        }
+        Check(hipStreamSynchronize(sp.prod), "sync prod");
+        Check(hipStreamSynchronize(sp.cons), "sync cons");
+        const auto t1 = Clock::now();
+        if (r >= warmup) samples.push_back(Us(t0, t1) / n);
+    }
+    std::vector<int32_t> host(size_t(n) * kWords);
+    Check(hipMemcpy(host.data(), blocks, host.size() * 4, hipMemcpyDeviceToHost), "sync status copy");
+    *timeouts = 0;
+    for (int i = 0; i < n; ++i)
+        if (host[size_t(i) * kWords + kOffStatus] != 1) ++*timeouts;
+    return Median(samples);
+}
+
+int RunSyncBench(const std::string &out_path, int device)
+{
+    const int n = 256, rounds = 10;
+    Check(hipSetDevice(device), "hipSetDevice");
+    StreamPair sp;
+    sp.Create(device);
+    DevBuf ctrl(size_t(2 * n) * kWords * 4);
+    std::vector<hipEvent_t> events(n, nullptr);
+    for (auto &e : events) Check(hipEventCreateWithFlags(&e, hipEventDisableTiming), "sync event");
+    int to_none = 0, to_event = 0, to_flag = 0;
+    const double none = SyncBenchMode("nosync", n, rounds, 2, sp, ctrl, events, &to_none);
+    const double event = SyncBenchMode("event", n, rounds, 2, sp, ctrl, events, &to_event);
+    const double flag = SyncBenchMode("flag", n, rounds, 2, sp, ctrl, events, &to_flag);
+    for (auto e : events) (void)hipEventDestroy(e);
+    sp.Destroy();
+    Value r = Value::MakeObject();
+    r.Set("n", Value::MakeNumber(n));
+    r.Set("rounds", Value::MakeNumber(rounds));
+    r.Set("us_per_pair_nosync", Value::MakeNumber(none));
+    r.Set("us_per_pair_event", Value::MakeNumber(event));
+    r.Set("us_per_pair_flag", Value::MakeNumber(flag));
+    r.Set("event_minus_nosync_us", Value::MakeNumber(event - none));
+    r.Set("flag_minus_nosync_us", Value::MakeNumber(flag - none));
+    r.Set("timeouts_nosync", Value::MakeNumber(to_none));
+    r.Set("timeouts_event", Value::MakeNumber(to_event));
+    r.Set("timeouts_flag", Value::MakeNumber(to_flag));
+    std::ofstream f(out_path);
+    f << r.Dump() << "\n";
+    std::printf("sync bench: nosync %.3f us/pair (to %d), event %.3f (to %d), flag %.3f (to %d), "
+                "event-base %.3f, flag-base %.3f\n",
+                none, to_none, event, to_event, flag, to_flag, event - none, flag - none);
+    return 0;
+}
+
 int RunPlan(const char *schedule_json, int iters, int warmup, const char *devices, const char *mode,
             const char *out_json)
 {
     try {
+        if (const char *sync_out = std::getenv("NHP_SYNC_BENCH")) return RunSyncBench(sync_out, ParseDevice(devices));
         if (iters < 1 || warmup < 0) {
             std::fprintf(stderr, "kr_plan_run: iters must be >= 1 and warmup >= 0\n");
             return 2;

@@ -233,4 +233,25 @@ __device__ __forceinline__ void RelayArrive(const RelayPub &p, int tile)
     }
 }
 
+// RelayArrive that also returns to every thread this workgroup's place in
+// the tile's arrival order (0 .. arrivals - 1): a consumer run by the
+// producer's own workgroups splits its work by it. `slot` is an LDS int of
+// the calling kernel.
+__device__ __forceinline__ int RelayArriveIndexed(const RelayPub &p, int tile, int *slot)
+{
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this lane's stores are complete
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        int32_t *flag = p.ctrl + size_t(p.flag0 + tile) * kWords;
+        const int32_t t = __hip_atomic_fetch_add(flag + kOffArrive, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (t == p.arrivals - 1) {
+            StoreRelaxed(flag + kOffArrive, 0);
+            __hip_atomic_fetch_add(flag + kOffPublished, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        *slot = t;
+    }
+    __syncthreads();
+    return *slot;
+}
+
 }  // namespace kr

@@ -29,13 +29,47 @@ __device__ __forceinline__ uint4 LoadU128Dev(const void *base, int off)
 //   rstd = 1 / sqrt(mean(s^2) + eps)     -> rstd_out[0] (optional, fp32)
 //   y = bf16(gamma * bf16(s * rstd))
 // The sum of squares is accumulated per lane over its chunks in order, then
-// over the 64 lanes by the butterfly of WaveSum. B_DEV: b was written by
-// other workgroups of the running kernel (read at device scope). coh: store
-// at device scope (outputs a relay releases).
-template <int DT, int CPL, bool B_DEV>
-__device__ __forceinline__ void AddRmsNormRow(const uint16_t *a, const uint16_t *b, const uint16_t *gamma,
-                                              uint16_t *y, uint16_t *sum, float *rstd_out, int cols, float eps,
-                                              int ln, bool coh)
+// over the 64 lanes by the butterfly of WaveSum. Split into load steps and a
+// finish step: the loads are branch-free (a lane's chunks past the row end
+// re-read its last chunk and are never used), so several rows' loads and
+// gamma stay in flight together and the finish step waits only for its own
+// row's data, never for earlier rows' stores.
+template <int CPL>
+struct RowIn {
+    uint4 a[CPL];
+    uint4 b[CPL];
+};
+
+__device__ __forceinline__ int RowChunk(int ln, int c, int chunks) { return min(ln + c * 64, chunks - 1); }
+
+template <int CPL>
+__device__ __forceinline__ void RowGammaLoad(const uint16_t *gamma, int cols, int ln, uint4 (&g)[CPL])
+{
+#pragma unroll
+    for (int c = 0; c < CPL; ++c) g[c] = *reinterpret_cast<const uint4 *>(gamma + RowChunk(ln, c, cols / 8) * 8);
+}
+
+// B_DEV: b was written by other workgroups of the running kernel (read at
+// device scope; b must be wave-uniform).
+template <int CPL, bool B_DEV>
+__device__ __forceinline__ void AddRmsNormLoad(const uint16_t *a, const uint16_t *b, int cols, int ln, RowIn<CPL> &in)
+{
+#pragma unroll
+    for (int c = 0; c < CPL; ++c) {
+        const int ch = RowChunk(ln, c, cols / 8);
+        in.a[c] = *reinterpret_cast<const uint4 *>(a + ch * 8);
+        if constexpr (B_DEV) {
+            in.b[c] = LoadU128Dev(b, ch * 16);
+        } else {
+            in.b[c] = *reinterpret_cast<const uint4 *>(b + ch * 8);
+        }
+    }
+}
+
+// coh: store at device scope (outputs a relay releases).
+template <int DT, int CPL>
+__device__ __forceinline__ void AddRmsNormFinish(const RowIn<CPL> &in, const uint4 (&g)[CPL], uint16_t *y,
+                                                 uint16_t *sum, float *rstd_out, int cols, float eps, int ln, bool coh)
 {
     const int chunks = cols / 8;
     float v[CPL][8];
@@ -45,14 +79,9 @@ __device__ __forceinline__ void AddRmsNormRow(const uint16_t *a, const uint16_t 
         const int ch = ln + c * 64;
         ok[c] = ch < chunks;
         if (ok[c]) {
-            const U16x8 x = LoadU16x8(a + ch * 8);
-            U16x8 w;
-            if constexpr (B_DEV) {
-                *reinterpret_cast<uint4 *>(w.v) = LoadU128Dev(b, ch * 16);
-            } else {
-                w = LoadU16x8(b + ch * 8);
-            }
-            U16x8 s;
+            U16x8 x, w, s;
+            *reinterpret_cast<uint4 *>(x.v) = in.a[c];
+            *reinterpret_cast<uint4 *>(w.v) = in.b[c];
 #pragma unroll
             for (int e = 0; e < 8; ++e) {
                 s.v[e] = Elem<DT>::Store(Elem<DT>::Load(x.v[e]) + Elem<DT>::Load(w.v[e]));
@@ -75,13 +104,24 @@ __device__ __forceinline__ void AddRmsNormRow(const uint16_t *a, const uint16_t 
 #pragma unroll
     for (int c = 0; c < CPL; ++c) {
         if (!ok[c]) continue;
-        const int ch = ln + c * 64;
-        const U16x8 g = LoadU16x8(gamma + ch * 8);
-        U16x8 o;
+        U16x8 gv, o;
+        *reinterpret_cast<uint4 *>(gv.v) = g[c];
 #pragma unroll
-        for (int e = 0; e < 8; ++e) o.v[e] = Elem<DT>::Store(Elem<DT>::Load(g.v[e]) * RoundTo<DT>(v[c][e] * rstd));
-        PutU128(y + ch * 8, *reinterpret_cast<const uint4 *>(o.v), coh);
+        for (int e = 0; e < 8; ++e) o.v[e] = Elem<DT>::Store(Elem<DT>::Load(gv.v[e]) * RoundTo<DT>(v[c][e] * rstd));
+        PutU128(y + (ln + c * 64) * 8, *reinterpret_cast<const uint4 *>(o.v), coh);
     }
+}
+
+template <int DT, int CPL, bool B_DEV>
+__device__ __forceinline__ void AddRmsNormRow(const uint16_t *a, const uint16_t *b, const uint16_t *gamma,
+                                              uint16_t *y, uint16_t *sum, float *rstd_out, int cols, float eps,
+                                              int ln, bool coh)
+{
+    uint4 g[CPL];
+    RowGammaLoad<CPL>(gamma, cols, ln, g);
+    RowIn<CPL> in;
+    AddRmsNormLoad<CPL, B_DEV>(a, b, cols, ln, in);
+    AddRmsNormFinish<DT, CPL>(in, g, y, sum, rstd_out, cols, eps, ln, coh);
 }
 
 // Chunks per lane of a one-wave row of `cols` 16-bit values, as the row

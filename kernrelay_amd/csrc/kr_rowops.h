@@ -15,7 +15,7 @@ enum EwOp : int {
     kEwSwiglu = 5,
     kEwSwigluGU = 6,  // x0 = fused [rows, 2*cols] gate/up, interleaved in groups of 8 columns
 };
-enum RowOp : int { kRowSoftmax = 0, kRowRmsNorm = 1, kRowAddRmsNorm = 2 };
+enum RowOp : int { kRowSoftmax = 0, kRowRmsNorm = 1, kRowAddRmsNorm = 2, kRowLayerNorm = 3 };
 
 // Elementwise op over a [rows, cols] tensor (cols % 8 == 0).
 //   gelu/silu/cast : y = f(x0)
@@ -39,6 +39,8 @@ struct EwDesc {
 //   softmax     : y = softmax(x0) along cols
 //   rmsnorm     : y = bf16(gamma * bf16(x0 * rstd)), rstd = 1/sqrt(mean(x0^2)+eps)
 //   add_rmsnorm : s = bf16(x0 + x1); y = rmsnorm(s); sum_out = s
+//   layernorm   : y = (x0 - mean) / sqrt(var + eps) * gamma + x1 (x1 = the
+//                 bias [cols]; biased variance, one rounding)
 // rstd_out (fp32 [rows]) and sum_out are optional.
 struct RowDesc {
     int op = kRowSoftmax;

@@ -233,6 +233,37 @@ __global__ void __launch_bounds__(kThreads) RowKernel(RowParams p)
                     for (int e = 0; e < 8; ++e) o.v[e] = Elem<DT>::Store(v[c][e] * inv);
                     PutU128(p.y + base + (ln + c * LPR) * 8, *reinterpret_cast<const uint4 *>(o.v), coh);
                 }
+            } else if constexpr (OP == kRowLayerNorm) {
+                // mean, then the biased variance about it (two passes over
+                // the registers), then one rounding of the affine result
+                float s1 = 0.0f;
+#pragma unroll
+                for (int c = 0; c < CPL; ++c)
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) s1 += v[c][e];
+                const float mean = GroupReduce<LPR, false>(s1, red) / float(p.cols);
+                float s2 = 0.0f;
+#pragma unroll
+                for (int c = 0; c < CPL; ++c)
+                    if (ok[c])
+#pragma unroll
+                        for (int e = 0; e < 8; ++e) {
+                            const float d = v[c][e] - mean;
+                            s2 += d * d;
+                        }
+                const float rstd = 1.0f / sqrtf(GroupReduce<LPR, false>(s2, red) / float(p.cols) + p.eps);
+                if (p.rstd_out != nullptr && active && ln == 0) PutU32(p.rstd_out + r, __float_as_uint(rstd), coh);
+#pragma unroll
+                for (int c = 0; c < CPL; ++c) {
+                    if (!ok[c]) continue;
+                    const int ch = ln + c * LPR;
+                    const U16x8 g = LoadU16x8(p.gamma + ch * 8), bb = LoadU16x8(p.x1 + ch * 8);
+                    U16x8 o;
+#pragma unroll
+                    for (int e = 0; e < 8; ++e)
+                        o.v[e] = Elem<DT>::Store((v[c][e] - mean) * rstd * Elem<DT>::Load(g.v[e]) + Elem<DT>::Load(bb.v[e]));
+                    PutU128(p.y + base + ch * 8, *reinterpret_cast<const uint4 *>(o.v), coh);
+                }
             } else {
                 float ss = 0.0f;
 #pragma unroll
@@ -542,6 +573,7 @@ void RowLaunch(const RowDesc &d, hipStream_t stream)
     CheckAligned(d.x0, "row op x0");
     CheckAligned(d.y, "row op y");
     if (d.op == kRowAddRmsNorm) CheckAligned(d.x1, "add_rmsnorm x1");
+    if (d.op == kRowLayerNorm) CheckAligned(d.x1, "layernorm bias");
     if (d.op != kRowSoftmax) CheckAligned(d.gamma, "rmsnorm gamma");
     if (d.sum_out) CheckAligned(d.sum_out, "add_rmsnorm sum");
     RowParams p{};
@@ -573,6 +605,7 @@ void RowLaunch(const RowDesc &d, hipStream_t stream)
         case kRowSoftmax: return RowDispatch<kRowSoftmax>(d, p, lpr, cpl, grid, stream);
         case kRowRmsNorm: return RowDispatch<kRowRmsNorm>(d, p, lpr, cpl, grid, stream);
         case kRowAddRmsNorm: return RowDispatch<kRowAddRmsNorm>(d, p, lpr, cpl, grid, stream);
+        case kRowLayerNorm: return RowDispatch<kRowLayerNorm>(d, p, lpr, cpl, grid, stream);
         default: throw std::runtime_error("row op: unknown op");
     }
 }

@@ -11,7 +11,7 @@ from . import libapi
 
 KR_BF16, KR_F16, KR_F32 = 0, 1, 2
 EW = {"gelu": 0, "silu": 1, "cast": 2, "mul": 3, "add": 4, "swiglu": 5, "swiglu_gu": 6}
-ROW = {"softmax": 0, "rmsnorm": 1, "add_rmsnorm": 2}
+ROW = {"softmax": 0, "rmsnorm": 1, "add_rmsnorm": 2, "layernorm": 3}
 CTRL_WORDS = 8
 
 

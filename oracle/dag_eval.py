@@ -91,7 +91,10 @@ def node_outputs(sched, rank=0, rows=None):
         def gamma():
             return _input(n, "gamma", C, (seed + 2) & 0xFFFFFFFF, dt)
 
-        eps = float(n.get("eps", 1e-6))
+        def beta():
+            return _input(n, "beta", C, (seed + 3) & 0xFFFFFFFF, dt)
+
+        eps = float(n.get("eps", 1e-5 if op == "layernorm" else 1e-6))
         if op == "matmul":
             K, N = int(n["k"]), int(n["n"])
             b = _input(n, "b", K * N, (seed + 2) & 0xFFFFFFFF, dt).reshape(K, N)
@@ -115,6 +118,8 @@ def node_outputs(sched, rank=0, rows=None):
             y, _ = ops.rmsnorm(x, gamma(), eps, tdt)
         elif op == "add_rmsnorm":
             y, _, _ = ops.add_rmsnorm(x, second(), gamma(), eps, tdt)
+        elif op == "layernorm":
+            y = ops.layernorm(x, gamma(), beta(), eps, tdt)
         else:
             raise ValueError("op %s has no oracle" % op)
         outs[n["id"]] = y

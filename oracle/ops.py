@@ -18,6 +18,8 @@ libraries, so the restatement follows the call sites and HF's definitions):
   rmsnorm     aclnnRmsNorm (:531-546), HF Qwen2RMSNorm: fp32 variance,
               x*rsqrt(var+eps) rounded, then times gamma
   add_rmsnorm aclnnAddRmsNorm (:548-565): sum rounded, then rmsnorm of it
+  layernorm   aclnnLayerNorm (exec/runtime/op_impl.cpp:237-254): biased
+              variance, eps 1e-5, weight and bias, one rounding
   rope        aclnnApplyRotaryPosEmb layout 1 (:567-582), rotate-half with
               tables from export_model.py:70-77; fp32, one rounding
   attention   aclnnFlashAttentionScore (:591-614): causal (MakeMask :487-497),
@@ -98,6 +100,16 @@ def add_rmsnorm(a, b, gamma, eps, dt=torch.bfloat16):
     s = add(a, b, dt)
     y, rstd = rmsnorm(s, gamma, eps, dt)
     return y, s, rstd
+
+
+def layernorm(x, weight, bias, eps=1e-5, dt=torch.bfloat16):
+    """aclnnLayerNorm over the last dim (exec/runtime/op_impl.cpp:237-254,
+    eps 1e-5 there): (x - mean) / sqrt(var + eps) * weight + bias, biased
+    variance, fp32, one rounding to the storage type."""
+    x = x.to(F32)
+    mean = x.mean(dim=-1, keepdim=True)
+    var = (x - mean).pow(2).mean(dim=-1, keepdim=True)
+    return rnd((x - mean) * torch.rsqrt(var + eps) * weight.to(F32) + bias.to(F32), dt)
 
 
 def rope_tables(max_pos, D, theta):

@@ -228,3 +228,121 @@ def even_ranges(rows, groups):
     """Consumer workgroup row ranges: ``groups`` near-equal slices."""
     b = [rows * i // groups for i in range(groups + 1)]
     return [(b[i], b[i + 1]) for i in range(groups)]
+
+
+# ------------------------------- consumer in the producer's workgroups ----
+
+class InProducerRelay:
+    """The relay consumer run by the producer's own workgroups (kr_gemm.hip
+    NormTail): each of a tile's ``arrivals`` workgroups writes its share of
+    the tile's rows, arrives with an indexed ticket (RelayArriveIndexed) —
+    the last one releases — then spins until ``published >= consumed + 1``,
+    reads the rows worker, worker + arrivals, ... of the whole tile (its
+    ticket is its worker index), and takes a done ticket; the last one
+    advances ``consumed`` and writes ``status``. One control block per tile
+    serves both roles, as a 1:1 edge does."""
+
+    def __init__(self, tiles, rows, arrivals, max_spins=200000, mistake=None):
+        self.tiles, self.rows_per_tile, self.arrivals = tiles, rows, arrivals
+        self.max_spins, self.mistake = max_spins, mistake
+        self.ctrl = Ctrl(tiles)
+        self.rows = [-1] * (tiles * rows)
+
+    def workgroup(self, replay, t, w, jitter, seen, write_delay=0.0):
+        c, base = self.ctrl, t * self.rows_per_tile
+        per = self.rows_per_tile // self.arrivals
+        lo = base + w * per
+        hi = base + (self.rows_per_tile if w == self.arrivals - 1 else (w + 1) * per)
+        if write_delay:
+            time.sleep(write_delay * w)
+        for r in range(lo, hi):
+            self.rows[r] = replay
+            _yield(jitter)
+        worker = c.fetch_add(t, OFF_ARRIVE, 1)
+        if worker == self.arrivals - 1:
+            c.store(t, OFF_ARRIVE, 0)
+            c.fetch_add(t, OFF_PUBLISHED, 1)
+        if self.mistake != "no_wait":
+            target = c.load(t, OFF_CONSUMED) + 1
+            spins = 0
+            while c.load(t, OFF_PUBLISHED) < target:
+                spins += 1
+                if spins > self.max_spins:
+                    c.store(t, OFF_TIMED_OUT, 1)
+                    break
+                time.sleep(0)
+        for r in range(base + worker, base + self.rows_per_tile, self.arrivals):
+            seen.append((r, self.rows[r], replay))
+            _yield(jitter)
+        if c.fetch_add(t, OFF_DONE, 1) == self.arrivals - 1:
+            c.store(t, OFF_DONE, 0)
+            to = c.exchange(t, OFF_TIMED_OUT, 0)
+            c.store(t, OFF_CONSUMED, c.load(t, OFF_CONSUMED) + 1)
+            c.store(t, OFF_STATUS, 2 if to else 1)
+
+    def replay(self, replay, jitter=0.2, write_delay=0.0):
+        """All workgroups as threads, started in random order; with
+        write_delay, workgroup w starts writing w * write_delay seconds late."""
+        seen = []
+        ids = [(t, w) for t in range(self.tiles) for w in range(self.arrivals)]
+        random.shuffle(ids)
+        jobs = [threading.Thread(target=self.workgroup, args=(replay, t, w, jitter, seen, write_delay))
+                for t, w in ids]
+        for th in jobs:
+            th.start()
+        for th in jobs:
+            th.join()
+        return seen
+
+
+# ------------------------------------------ last-arrival fix-up of pieces ----
+
+class PieceFixup:
+    """Split work summed by its last piece (the stream-K GEMM's fix-up in
+    kr_gemm_pipe.inc, the split attention's in kr_attn.hip): each of ``n``
+    pieces writes its partial, waits for its own stores, then takes a ticket
+    on the tile's counter; the piece that draws n - 1 resets the counter and
+    sums every partial in piece order. The sum must use each piece's value of
+    the current launch, and the order must not depend on which piece was
+    last."""
+
+    def __init__(self, pieces, mistake=None):
+        self.n, self.mistake = pieces, mistake
+        self.partial = [None] * pieces
+        self.count = 0
+        self._lock = threading.Lock()
+        self.result = None
+
+    def piece(self, launch, i, jitter, store_delay=0.0):
+        value = (launch, i)
+        if self.mistake == "ticket_before_store":
+            # the ticket goes out while the partial is still being written
+            ticket = self._ticket()
+            if ticket != self.n - 1:
+                time.sleep(store_delay)
+            self.partial[i] = value
+        else:
+            _yield(jitter)
+            self.partial[i] = value
+            ticket = self._ticket()
+        if ticket == self.n - 1:
+            with self._lock:
+                self.count = 0
+            order = range(self.n) if self.mistake != "arrival_order" else [i] + [j for j in range(self.n) if j != i]
+            self.result = [self.partial[j] for j in order]
+
+    def _ticket(self):
+        with self._lock:
+            t = self.count
+            self.count += 1
+            return t
+
+    def launch(self, launch, jitter=0.3, store_delay=0.0):
+        self.result = None
+        ths = [threading.Thread(target=self.piece, args=(launch, i, jitter, store_delay)) for i in range(self.n)]
+        random.shuffle(ths)
+        for th in ths:
+            th.start()
+        for th in ths:
+            th.join()
+        return self.result

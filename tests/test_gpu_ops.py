@@ -222,6 +222,23 @@ def test_rmsnorm_and_add_rmsnorm(gpu, cols):
     assert torch.equal(y2, y)  # fused and separate paths agree bit for bit
 
 
+@pytest.mark.parametrize("cols,dt", [(2048, torch.float16), (3584, torch.bfloat16), (896, torch.bfloat16),
+                                     (128, torch.float16), (8192, torch.bfloat16)])
+def test_layernorm(gpu, cols, dt):
+    """LayerNorm (aclnnLayerNorm, reference exec/runtime/op_impl.cpp:237-254:
+    weight, bias, eps 1e-5) against the oracle, one-wave rows, 16-lane rows and
+    whole-workgroup rows."""
+    announce("layernorm cols=%d %s" % (cols, dt))
+    rows = 333
+    x = rand((rows, cols), 2.0, 81, dt) + 0.25
+    w, b = rand((cols,), 1.0, 82, dt), rand((cols,), 1.0, 83, dt)
+    y = torch.empty(rows, cols, dtype=dt, device="cuda")
+    xc = x.to(dt).cuda()
+    ops.rowop("layernorm", xc, y, x1=b.cuda(), gamma=w.cuda(), eps=1e-5)
+    torch.cuda.synchronize()
+    close(y, O.layernorm(x.float(), w.float(), b.float(), 1e-5, dt))
+
+
 def test_rope(gpu):
     announce("rope")
     S, Hh, D = 160, 3, 128

@@ -11,7 +11,7 @@ import torch
 from kernrelay_amd import libapi, schedule, workloads
 from oracle import dag_eval
 from tests.conftest import announce
-from tests.test_oracle_dag import KATS, ref_dag
+from tests.test_oracle_dag import KATS, kat_dag, ln_mm_dag, ref_dag
 
 pytestmark = pytest.mark.gpu
 
@@ -105,11 +105,12 @@ def test_mn_row_geometry(gpu, tmp_path, chunking):
         assert np.array_equal(base[k], outs[k]), (chunking, k)
 
 
-@pytest.mark.parametrize("name,consumers,expected", KATS[:3])
+@pytest.mark.parametrize("name,consumers,expected", KATS)
 def test_reference_checksums_on_gpu(gpu, tmp_path, name, consumers, expected):
     """The reference's own E3/E4 DAGs (fp16, 2 ranks, DetValue inputs) split at
-    k=4 reproduce its recorded checksums within its consistency gate."""
-    dag = ref_dag(name, consumers)
+    k=4 reproduce its recorded checksums within its consistency gate: mm ->
+    gelu / softmax / both / cast, and the reverse edge LayerNorm -> mm."""
+    dag = kat_dag(name, consumers)
     sched = schedule.build_fixed_schedule(dag, {n.name: 4 for n in dag.nodes}, nranks=2)
     path = schedule.dump_schedule(sched, tmp_path / "kat.json")
     announce("plan_run KAT " + name)
@@ -180,3 +181,45 @@ def test_fused_fanout_all_ops(gpu, tmp_path):
         for node in base:
             assert np.array_equal(base[node], outs[node]), (k, node)
     assert_close_to_oracle(schedule.serial_schedule(dag), outs)
+
+
+@pytest.mark.parametrize("k", [1, 2, 4, 8])
+def test_layernorm_to_gemm_relay(gpu, tmp_path, k):
+    """The reverse edge (the reference's dags/e3_ln_mm.json at 4096 rows): a
+    LayerNorm on the consumer stream releases k row tiles and the GEMM on the
+    producer stream waits for the tiles of A each of its tiles reads. Split
+    == serial bit for bit; both within the bf16 bar of the oracle."""
+    raw = {"name": "ln_mm", "nodes": [
+        {"name": "ln", "op": "layernorm", "engine": "aiv", "shape": {"rows": 4096, "cols": 2048}, "dtype": "bf16"},
+        {"name": "mm", "op": "matmul", "engine": "aic", "shape": {"M": 4096, "K": 2048, "N": 2048}, "dtype": "bf16"}],
+        "edges": [{"src": "ln", "dst": "mm", "kind": "data"}]}
+    dag = schedule.dag_from_dict(raw)
+    _, base = run(schedule.serial_schedule(dag), tmp_path, "serial")
+    r, outs = run(schedule.build_fixed_schedule(dag, {"ln": k, "mm": k}), tmp_path, "split%d" % k,
+                  mode="graph_per_stream")
+    assert r["gate_timeouts"] == 0
+    for name in ("ln", "mm"):
+        assert np.array_equal(outs[name], base[name]), name
+    assert_close_to_oracle(schedule.serial_schedule(dag), outs, rows=128)
+
+
+def test_sync_micro_benchmark(gpu, tmp_path):
+    """NHP_SYNC_BENCH (the reference's cross-stream sync micro-benchmark,
+    exec/exec_main.cpp:751-833): 256 publish/wait kernel pairs per round on
+    two hardware queues, without sync, with an event and with a device flag.
+    Every flag wait is released (status 1); the result has the reference's
+    keys."""
+    import json
+    out = tmp_path / "sync.json"
+    os.environ["NHP_SYNC_BENCH"] = str(out)
+    try:
+        announce("plan_run NHP_SYNC_BENCH")
+        rc = libapi.lib().kr_plan_run(b"unused", 1, 0, b"0", b"direct", str(tmp_path / "unused.json").encode())
+    finally:
+        del os.environ["NHP_SYNC_BENCH"]
+    assert rc == 0
+    r = json.loads(out.read_text())
+    assert r["n"] == 256 and r["timeouts_flag"] == 0 and r["timeouts_event"] == 0 and r["timeouts_nosync"] == 0
+    for k in ("us_per_pair_nosync", "us_per_pair_event", "us_per_pair_flag"):
+        assert r[k] > 0
+    announce("sync bench: %s" % json.dumps(r))

@@ -3,8 +3,9 @@
 results/final/e34_raw.json holds the reference executor's checksums for its
 E3/E4 DAGs (fp16, 2 ranks, DetValue inputs): mm->gelu 0.84616 (:15),
 mm->softmax 7.714923 (:2301), mm->{gelu,softmax} 8.846179 (:2969) and
-mm->cast 7405.689026. The oracle restatement must reproduce them; a wrong
-seed, input role, row order or op fails here.
+mm->cast 7405.689026 and LayerNorm->mm 5.91964 (:2003). The oracle
+restatement must reproduce them; a wrong seed, input role, row order or op
+(e.g. an unbiased variance or eps 1e-6 in the LayerNorm) fails here.
 """
 
 import numpy as np
@@ -31,12 +32,28 @@ KATS = [
     ("e3_mm_softmax", ["softmax"], 7.714923),
     ("f04_mm_fanout_c2", ["gelu", "softmax"], 8.846179),
     ("e3_mm_cast", ["cast"], 7405.689026),
+    ("e3_ln_mm", None, 5.91964),
 ]
+
+
+def ln_mm_dag():
+    """The reference's dags/e3_ln_mm.json: a LayerNorm producer on the vector
+    engine feeding a GEMM consumer (the reverse edge), 32768 x 2048, fp16;
+    its recorded checksum is results/final/e34_raw.json:2003 (5.91964)."""
+    return schedule.dag_from_dict({"name": "e3_ln_mm", "nodes": [
+        {"name": "ln", "op": "layernorm", "engine": "aiv", "shape": {"rows": 32768, "cols": 2048},
+         "dtype": "fp16", "tiles": 4},
+        {"name": "mm", "op": "matmul", "engine": "aic", "shape": {"M": 32768, "K": 2048, "N": 2048},
+         "dtype": "fp16", "tiles": 4}], "edges": [{"src": "ln", "dst": "mm", "kind": "data"}]})
+
+
+def kat_dag(name, consumers):
+    return ln_mm_dag() if consumers is None else ref_dag(name, consumers)
 
 
 @pytest.mark.parametrize("name,consumers,expected", KATS)
 def test_reference_checksums(name, consumers, expected):
-    dag = ref_dag(name, consumers)
+    dag = kat_dag(name, consumers)
     sched = schedule.build_fixed_schedule(dag, {n.name: 4 for n in dag.nodes}, nranks=2)
     got = dag_eval.checksum(sched)
     # the reference prints 7 significant digits and computes with closed

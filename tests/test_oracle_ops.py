@@ -141,3 +141,14 @@ def test_embedding():
     t = bf(torch.randn(50, 16))
     ids = torch.tensor([3, 0, 49, 3])
     assert torch.equal(O.embedding(t, ids), t[ids])
+
+
+def test_layernorm_matches_library_and_rejects_variants():
+    x = bf(torch.randn(9, 2048) * 2 + 0.5)
+    w, b = bf(torch.randn(2048)), bf(torch.randn(2048))
+    ref = F.layer_norm(x, (2048,), w, b, eps=1e-5)
+    assert torch.allclose(O.layernorm(x, w, b, 1e-5, torch.float32), ref, atol=2e-5, rtol=1e-5)
+    # unbiased variance or a dropped bias are visible
+    unbiased = (x - x.mean(-1, keepdim=True)) / torch.sqrt(x.var(-1, unbiased=True, keepdim=True) + 1e-5) * w + b
+    assert not torch.allclose(O.layernorm(x, w, b, 1e-5, torch.float32), unbiased, atol=1e-5)
+    assert not torch.allclose(O.layernorm(x, w, torch.zeros_like(b), 1e-5, torch.float32), ref, atol=1e-2)
