@@ -155,6 +155,42 @@ def profile_gemm_swiglu(M, I, K, reps):
     print("gemm+swiglu %dx%dx%d x%d done" % (M, 2 * I, K, reps), flush=True)
 
 
+def profile_consumers(reps):
+    """One launch per repetition of each consumer kernel and of attention at
+    the shapes the relay path runs them (the program the rocprofv3 --pmc
+    passes of the consumer traffic and the attention counters run):
+    row softmax, GELU and bf16->fp16 cast over [4096, 4096] (the fan-out
+    DAG's consumers), Add+RMSNorm over
+    [2048, 3584] (the 7B residual) and causal attention at 28 query / 4 kv
+    heads x 2048 x 128 (the 7B layer)."""
+    import torch
+
+    from kernrelay_amd import ops
+
+    g = torch.Generator(device="cuda").manual_seed(9)
+    x = torch.randn(4096, 4096, device="cuda", generator=g).to(torch.bfloat16)
+    y = torch.empty_like(x)
+    yh = torch.empty(4096, 4096, device="cuda", dtype=torch.float16)
+    a = torch.randn(2048, 3584, device="cuda", generator=g).to(torch.bfloat16)
+    b = torch.randn(2048, 3584, device="cuda", generator=g).to(torch.bfloat16)
+    gam = torch.ones(3584, device="cuda", dtype=torch.bfloat16)
+    ny, ns = torch.empty_like(a), torch.empty_like(a)
+    rstd = torch.empty(2048, device="cuda")
+    S, HQ, HKV, D = 2048, 28, 4, 128
+    qkv = torch.randn(S, (HQ + 2 * HKV) * D, device="cuda", generator=g).to(torch.bfloat16)
+    ld = qkv.stride(0)
+    q, k, v = qkv[:, :HQ * D], qkv[:, HQ * D:(HQ + HKV) * D], qkv[:, (HQ + HKV) * D:]
+    att = torch.empty(S, HQ * D, device="cuda", dtype=torch.bfloat16)
+    for _ in range(reps):
+        ops.rowop("softmax", x, y)
+        ops.elementwise("gelu", x, y)
+        ops.elementwise("cast", x, yh)
+        ops.rowop("add_rmsnorm", a, ny, x1=b, gamma=gam, sum_out=ns, rstd_out=rstd)
+        ops.attention(q, k, v, att, S, HQ, HKV, D, ldq=ld, ldk=ld, ldv=ld)
+    torch.cuda.synchronize()
+    print("consumers + attention x%d done" % reps, flush=True)
+
+
 def profile_copy(mib, reps):
     """A plain device copy of known size: what FETCH_SIZE / WRITE_SIZE read
     for it calibrates the counters."""
@@ -187,6 +223,8 @@ def main():
     ap.add_argument("--profile-gemm-swiglu", nargs=3, type=int, metavar=("M", "I", "K"),
                     help="only launch the gate/up GEMM with SwiGLU epilogue --reps times (for rocprofv3 --pmc)")
     ap.add_argument("--profile-copy", type=int, metavar="MIB", help="only copy MIB MiB --reps times")
+    ap.add_argument("--profile-consumers", action="store_true",
+                    help="only launch the consumer kernels and attention --reps times (for rocprofv3 --pmc)")
     ap.add_argument("--reps", type=int, default=3)
     args = ap.parse_args()
     if args.profile_gemm:
@@ -197,6 +235,9 @@ def main():
         return
     if args.profile_copy:
         profile_copy(args.profile_copy, args.reps)
+        return
+    if args.profile_consumers:
+        profile_consumers(args.reps)
         return
     if args.gpus != 1:
         print("bench.py: this build targets one GPU; --gpus %d is not supported (the relay path is "
