@@ -4,28 +4,40 @@
 // exec/qwen_main.cpp:591-614: scale 1/sqrt(D), keepProb 1, sparseMode 3 with
 // the upper-triangular mask of MakeMask :487-497).
 //
-// One workgroup = 128 queries of one head (4 waves x 32 queries); keys and
-// values stream through a double-buffered LDS ring in blocks of 64: block
-// kb+1 is loaded into registers while block kb is computed, then written to
-// the other buffer, one barrier per block. The kernel computes the
-// transposed products so that every operand lands where the next MFMA wants
-// it, with no cross-lane shuffles of P:
-//   S^T = K . Q^T   (32x32x16: A = K rows from LDS, B = Q rows in registers)
-//       -> lane l holds query l%32 and 16 keys of each 32-key half; the row
-//          max / sum over keys is a lane-local loop plus one xor-32 shuffle.
-//   O^T += V^T . P^T (A = V^T from a transposed LDS copy, B = P^T straight
-//          from the S^T accumulators after rounding to 16 bits).
-// MFMA pairs A slot s with B slot s, so the key order inside a 16-key step
-// only has to agree between V^T and P^T. P^T's order is the accumulator's
-// {4h..4h+3, 8+4h..8+4h+3} for lane half h; V^T rows are stored with the keys
-// of each 16-key group permuted into exactly that order, so one ds_read_b128
-// fetches a lane's 8 keys.
+// One workgroup = 128 queries of one head (4 waves x 32 queries) times KH
+// key halves: with KH = 2 the workgroup has 8 waves, and waves 4..7 take the
+// odd 64-key blocks of the same 128 queries while waves 0..3 take the even
+// ones, merging their (m, l, O) through LDS at the end; that halves the
+// longest causal row's walk, the critical path of a causal grid.
+//
+// Keys and values go global -> LDS by the direct-to-LDS DMA (kr_dma.h), both
+// row-major, into a two-stage ring: stage s+1 is fetched while stage s is
+// computed, one wait + barrier per stage, no VGPR staging. The 16-byte
+// chunks of each row are XOR-swizzled on the source side (each DMA lane
+// picks the chunk its LDS slot holds) so that the fragment reads below hit
+// distinct banks.
+//
+// Products, chosen so that every operand lands where the next MFMA wants it:
+//   S^T = K . Q^T   (v_mfma_f32_32x32x16: A = K rows by ds_read_b128, B = Q
+//       rows held in registers) -> lane l holds query l % 32 and 16 keys of
+//       each 32-key half; the row max / sum is a lane-local loop plus one
+//       xor-32 shuffle.
+//   O^T += V^T . P^T (A = V^T by ds_read_b64_tr_b16 from the row-major V,
+//       B = P^T straight from the S^T accumulators rounded to 16 bits).
+// ds_read_b64_tr_b16 hands lane 4a+b of each 16-lane group element b of the
+// 8-byte pieces addressed by lanes a, a+4, a+8, a+12; when lane s addresses
+// V row k0 + s/4, columns d0 + 4 (s%4).., lane j receives V[k0..k0+3][d0+j],
+// a column of V: the A operand's four keys. Two such reads give a lane its
+// 8 keys, placed in the accumulator order of P^T ({4h..4h+3, 8+4h..8+4h+3}
+// for lane half h; MFMA pairs A slot i with B slot i, so only the two sides'
+// key orders have to agree).
 // Online softmax in base 2 (exponent fma(score, scale*log2(e), -m)), fp32
 // state, with the running max m moved lazily (see the loop).
 // Workgroups run heaviest (longest causal rows) first across all heads.
 #include <algorithm>
 #include <vector>
 
+#include "kr_dma.h"
 #include "kr_misc.h"
 
 namespace kr {
@@ -35,9 +47,11 @@ namespace {
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef short AttnS4 __attribute__((ext_vector_type(4)));
+typedef uint32_t AttnU2 __attribute__((ext_vector_type(2)));
+typedef __attribute__((address_space(3))) AttnS4 *LdsS4;
 
 constexpr int kKvBlk = 64;
-typedef uint32_t AttnU32x4 __attribute__((ext_vector_type(4)));
 
 // two values to 16 bits (round to nearest even, as Elem<DT>::Store), packed
 // low | high << 16: one v_cvt_pk_bf16_f32 for bf16
@@ -75,8 +89,41 @@ struct AttnParams {
     float *ws;       // split partials [sid][HQ][pmax][chunks][256 threads][4]
     int32_t *cnt;    // [sid][HQ] arrival tickets, zero between launches
     int pmax;
+    // workgroup -> (item, head): xcds 0 = b / HQ, b % HQ; otherwise the 8
+    // XCDs (workgroup b runs on XCD b % 8) are shared out by kv head so that
+    // one XCD's L2 holds the keys and values of only its own kv heads
+    int xcds, nitems;
     AttnItem items[kMaxItems];
 };
+
+// Workgroup b -> (item index, query head). XCD x = b % 8 serves kv head
+// x / (8 / HKV) when HKV divides 8 (its share of that head's (item, query
+// head) units, heaviest items first), or kv heads x, x + 8, ... when 8
+// divides HKV. Returns false for the padding workgroups of the last round.
+__device__ __forceinline__ bool AttnUnit(const AttnParams &p, int b, int &item, int &h)
+{
+    if (p.xcds == 0) {
+        h = b % p.HQ;
+        item = b / p.HQ;
+        return true;
+    }
+    const int x = b % p.xcds, i = b / p.xcds;
+    const int gq = p.HQ / p.HKV;  // query heads per kv head
+    int kv, u;
+    if (p.HKV <= p.xcds) {
+        const int r = p.xcds / p.HKV;  // XCDs per kv head
+        kv = x / r;
+        u = i * r + x % r;
+        item = u / gq;
+        h = kv * gq + u % gq;
+    } else {
+        const int per = p.HKV / p.xcds;  // kv heads per XCD
+        item = i / (per * gq);
+        const int rem = i % (per * gq);
+        h = (x + p.xcds * (rem / gq)) * gq + rem % gq;
+    }
+    return item < p.nitems;
+}
 
 template <int DT>
 __device__ __forceinline__ f32x16 Mfma(const uint4 &a, const uint4 &b, const f32x16 &c)
@@ -90,39 +137,51 @@ __device__ __forceinline__ f32x16 Mfma(const uint4 &a, const uint4 &b, const f32
     }
 }
 
+// LDS slot of 16-byte chunk c in row r of a K / V block (an XOR, so it also
+// maps a slot back to its chunk). K (D/8 chunks a row, read 16 rows x one
+// chunk per 16 lanes): rows 0..15 of a pass land in 16 distinct slots of the
+// 256-byte bank line. V (read by ds_read_b64_tr_b16: 4 rows x 4 chunks per
+// 16 lanes): the four rows of a read land in four distinct chunk groups.
 template <int D>
-__device__ __forceinline__ int KSwz(int r, int c)
+__device__ __forceinline__ int KSlot(int r, int c)
 {
     if constexpr (D == 128) return c ^ (r & 15);
     else return c ^ ((r >> 1) & 7);
 }
-
-// V^T rows hold 64 keys = 8 chunks of 16 bytes; chunk c of row d sits in
-// slot c ^ VSwz(d) (distinct slots for 8- and 16-lane passes).
-__device__ __forceinline__ int VSwz(int d) { return (d & 7) ^ ((d >> 3) & 1); }
-
-template <int DT, int D>
-__global__ void __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_waves_per_eu(2))) AttnKernel(AttnParams p)
+template <int D>
+__device__ __forceinline__ int VSlot(int r, int c)
 {
-    constexpr int DCH = D / 8;                       // 16-byte chunks per K/V row
-    constexpr int DBLK = D / 32;
-    constexpr int KL = kKvBlk * DCH / 256;           // K chunks per thread per block
-    constexpr int VG = (kKvBlk / 4) * DCH;           // V (4 keys x 8 d) groups per block
-    constexpr int VL = (VG + 255) / 256;             // V groups per thread
-    __shared__ __attribute__((aligned(16))) uint16_t Ks[2][kKvBlk * D];
-    __shared__ __attribute__((aligned(16))) uint16_t Vt[2][D * kKvBlk];
+    if constexpr (D == 128) return c ^ (4 * (r & 3));
+    else return c ^ (4 * ((r >> 1) & 1));
+}
 
+template <int DT, int D, int KH>
+__global__ void __attribute__((amdgpu_flat_work_group_size(256 * KH, 256 * KH), amdgpu_waves_per_eu(2)))
+AttnKernel(AttnParams p)
+{
+    static_assert(D == 64 || D == 128, "head_dim 64 or 128");
+    static_assert(KH == 1 || KH == 2, "one or two key halves");
+    constexpr int DCH = D / 8;             // 16-byte chunks per K/V row
+    constexpr int DBLK = D / 32;           // 32-wide d blocks of O^T
+    constexpr int BLK = kKvBlk * D;        // elements of one K or V block
+    constexpr int RPD = 64 / DCH;          // rows per 1 KB DMA block
+    constexpr int DPW = kKvBlk / RPD / 4;  // DMA blocks per wave per operand and block
+    // two-slot rings [slot][half]: K and V of stage s in slot s & 1
+    __shared__ __attribute__((aligned(1024))) uint16_t kring[2][KH][BLK];
+    __shared__ __attribute__((aligned(1024))) uint16_t vring[2][KH][BLK];
     __shared__ int last_piece;
-    const int tid = threadIdx.x;
+
+    const int hv = __builtin_amdgcn_readfirstlane(int(threadIdx.x) >> 8);  // key half
+    const int tid = int(threadIdx.x) & 255;
     const int lane = tid & 63;
-    const int wave = tid >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int hf = lane >> 5;
-    const int h = int(blockIdx.x) % p.HQ;
-    const AttnItem item = p.items[int(blockIdx.x) / p.HQ];
+    int item_ix, h;
+    if (!AttnUnit(p, int(blockIdx.x), item_ix, h)) return;  // whole workgroup, before any barrier
+    const AttnItem item = p.items[item_ix];
     const int qb = item.qb;
     const int q0 = qb * kQBlk;
     const int kvh = h / (p.HQ / p.HKV);
-    const int64_t ldq = p.ldq;
     const int qrow = q0 + wave * 32 + (lane & 31);
     const int wave_q_hi = min(q0 + wave * 32 + 31, p.S - 1);
 
@@ -130,7 +189,7 @@ __global__ void __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_wav
 #pragma unroll
     for (int dc = 0; dc < D / 16; ++dc) {
         if (qrow < p.S) {
-            qf[dc] = *reinterpret_cast<const uint4 *>(p.q + int64_t(qrow) * ldq + int64_t(h) * D + dc * 16 + hf * 8);
+            qf[dc] = *reinterpret_cast<const uint4 *>(p.q + int64_t(qrow) * p.ldq + int64_t(h) * D + dc * 16 + hf * 8);
         } else {
             qf[dc] = make_uint4(0, 0, 0, 0);
         }
@@ -144,180 +203,221 @@ __global__ void __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_wav
     float m = -INFINITY;
     float l = 0.0f;
 
-    const int kb_lo = item.kb_lo, kb_hi = item.kb_hi;
-
-    // block kb -> registers, with no branch around a load: rows past S read
-    // row S-1 again (their keys are masked to -inf, so their P is exactly 0
-    // and their finite K and V rows contribute nothing), threads past the
-    // block's V groups (D 64) read group 0 again and never store it. Plain
-    // vector types: struct copies would go through memcpy, which keeps the
-    // arrays in scratch memory.
-    AttnU32x4 kr[KL];
-    AttnU32x4 vr[VL][4];
-    // this thread's element offsets inside a block of K / V rows
-    int koff[KL], voff[VL][4];
+    // DMA geometry: this wave fills 1 KB blocks wave*DPW .. +DPW-1 of each
+    // K and V block; lane -> (row, slot), fetching the chunk the slot holds
+    const int drow = wave * DPW * RPD + lane / DCH;
+    const int dslot = lane % DCH;
+    int koff[DPW], voff[DPW];
 #pragma unroll
-    for (int i = 0; i < KL; ++i) {
-        const int t = tid + 256 * i;
-        koff[i] = (t / DCH) * int(p.ldk) + kvh * D + (t % DCH) * 8;
+    for (int j = 0; j < DPW; ++j) {
+        const int r = drow + j * RPD;
+        koff[j] = r * int(p.ldk) + kvh * D + KSlot<D>(r, dslot) * 8;
+        voff[j] = r * int(p.ldv) + kvh * D + VSlot<D>(r, dslot) * 8;
     }
-#pragma unroll
-    for (int i = 0; i < VL; ++i) {
-        const int t = tid + 256 * i;
-        const int grp = t < VG ? t / DCH : 0, c = t % DCH;
-#pragma unroll
-        for (int r = 0; r < 4; ++r) voff[i][r] = (4 * grp + r) * int(p.ldv) + kvh * D + c * 8;
-    }
-    auto load = [&](int kb) {
+    // block kb of K (or V) -> ring slot buf of this half
+    auto dma = [&](const uint16_t *src, int64_t ld, const int (&off)[DPW], uint32_t ring_base, int kb, int buf,
+                   bool vswz) {
         const int kv0 = kb * kKvBlk;
+        const uint32_t dst = ring_base + uint32_t((buf * KH + hv) * BLK * 2) + uint32_t(wave * DPW) * 1024u;
         if (kv0 + kKvBlk <= p.S) {
-            // a whole block inside S: the block's base plus this thread's offsets
-            const uint16_t *kbase = p.k + int64_t(kv0) * p.ldk;
-            const uint16_t *vbase = p.v + int64_t(kv0) * p.ldv;
+            const uint16_t *b0 = src + int64_t(kv0) * ld;
 #pragma unroll
-            for (int i = 0; i < KL; ++i) kr[i] = *reinterpret_cast<const AttnU32x4 *>(kbase + koff[i]);
-#pragma unroll
-            for (int i = 0; i < VL; ++i)
-#pragma unroll
-                for (int r = 0; r < 4; ++r) vr[i][r] = *reinterpret_cast<const AttnU32x4 *>(vbase + voff[i][r]);
+            for (int j = 0; j < DPW; ++j) DmaLoad16(b0 + off[j], dst + uint32_t(j) * 1024u);
             return;
         }
+        // rows past S re-read row S-1: their keys are masked to -inf, so
+        // their P is exactly 0 and their finite K and V contribute nothing
 #pragma unroll
-        for (int i = 0; i < KL; ++i) {
-            const int t = tid + 256 * i;
-            const int kv = min(kv0 + t / DCH, p.S - 1);
-            kr[i] = *reinterpret_cast<const AttnU32x4 *>(p.k + int64_t(kv) * p.ldk + int64_t(kvh) * D + (t % DCH) * 8);
-        }
-#pragma unroll
-        for (int i = 0; i < VL; ++i) {
-            const int t = tid + 256 * i;
-            const int grp = t < VG ? t / DCH : 0, c = t % DCH;
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int kv = min(kv0 + 4 * grp + r, p.S - 1);
-                vr[i][r] = *reinterpret_cast<const AttnU32x4 *>(p.v + int64_t(kv) * p.ldv + int64_t(kvh) * D + c * 8);
-            }
+        for (int j = 0; j < DPW; ++j) {
+            const int r = drow + j * RPD;
+            const int kv = min(kv0 + r, p.S - 1);
+            const int c = vswz ? VSlot<D>(r, dslot) : KSlot<D>(r, dslot);
+            DmaLoad16(src + int64_t(kv) * ld + int64_t(kvh) * D + c * 8, dst + uint32_t(j) * 1024u);
         }
     };
-    // registers -> LDS buffer b: K row-major (swizzled), V transposed with
-    // each 16-key group permuted to the P^T slot order
-    auto store = [&](int b) {
+    const uint32_t kring0 = LdsAddr(&kring[0][0][0]);
+    const uint32_t vring0 = LdsAddr(&vring[0][0][0]);
+
+    // fragment addresses (elements inside a K / V block)
+    // K: lane reads row kh*32 + lane%32, chunk 2 dc + hf
+    int kaddr[D / 16];
 #pragma unroll
-        for (int i = 0; i < KL; ++i) {
-            const int t = tid + 256 * i;
-            const int r = t / DCH, c = t % DCH;
-            *reinterpret_cast<AttnU32x4 *>(&Ks[b][r * D + KSwz<D>(r, c) * 8]) = kr[i];
+    for (int dc = 0; dc < D / 16; ++dc) {
+        const int r = lane & 31;  // (kh*32 keeps r & 15 and (r >> 1) & 7)
+        kaddr[dc] = r * D + KSlot<D>(r, 2 * dc + hf) * 8;
+    }
+    // V^T: lane s of 16-lane group g reads row c*16 + 8 rd + 4 hf + s/4,
+    // columns b*32 + 16 (g & 1) + 4 (s & 3)..; the row's low bits (and so
+    // the slot's XOR) do not depend on c or rd
+    int vaddr[DBLK];
+    {
+        const int s16 = lane & 15;
+        const int g1 = (lane >> 4) & 1;
+        const int row = 4 * hf + (s16 >> 2);
+#pragma unroll
+        for (int b = 0; b < DBLK; ++b) {
+            const int col = b * 32 + 16 * g1 + 4 * (s16 & 3);
+            vaddr[b] = row * D + VSlot<D>(row, col / 8) * 8 + (col & 7);
         }
+    }
+
+    // S^T of one block: 2 halves of 32 keys
+    auto qk = [&](const uint16_t *K, f32x16 (&sacc)[2]) {
+        uint4 kf[2][D / 16];
 #pragma unroll
-        for (int i = 0; i < VL; ++i) {
-            const int t = tid + 256 * i;
-            if (VG % 256 != 0 && t >= VG) continue;  // (D 64: half the threads)
-            const int ap = t / DCH, c = t % DCH;  // keys 4ap..4ap+3, d chunk c
-            const int u = 4 * (ap >> 2) + ((ap & 3) >> 1) + 2 * (ap & 1);  // 8-byte unit in the row
-            const AttnU32x4 &w0 = vr[i][0], &w1 = vr[i][1], &w2 = vr[i][2], &w3 = vr[i][3];
+        for (int dc = 0; dc < D / 16; ++dc)
+#pragma unroll
+            for (int kh = 0; kh < 2; ++kh) kf[kh][dc] = *reinterpret_cast<const uint4 *>(K + kh * 32 * D + kaddr[dc]);
+#pragma unroll
+        for (int kh = 0; kh < 2; ++kh)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) sacc[kh][v] = 0.0f;
+#pragma unroll
+        for (int dc = 0; dc < D / 16; ++dc)
+#pragma unroll
+            for (int kh = 0; kh < 2; ++kh) sacc[kh] = Mfma<DT>(kf[kh][dc], qf[dc], sacc[kh]);
+    };
+    // causal / past-S mask of one block's raw scores: register v of half kh
+    // holds key kv0 + kh*32 + 8 (v/4) + 4 hf + v%4, masked to -inf when that
+    // exceeds min(qrow, S-1): one compare with a constant
+    auto mask = [&](f32x16 (&sacc)[2], int kv0) {
+        if (kv0 + kKvBlk - 1 > q0 + wave * 32 || kv0 + kKvBlk > p.S) {
+            const int lim = min(qrow, p.S - 1) - kv0 - 4 * hf;
+#pragma unroll
+            for (int kh = 0; kh < 2; ++kh)
+#pragma unroll
+                for (int v = 0; v < 16; ++v)
+                    sacc[kh][v] = kh * 32 + 8 * (v >> 2) + (v & 3) > lim ? -INFINITY : sacc[kh][v];
+        }
+    };
+    // softmax of one block's masked scores -> P^T packed to 16 bits (pf[c]:
+    // keys of 16-key step c in the accumulator order), running (m, l);
+    // returns the O rescale factor (1 unless the row max moved). The row max
+    // is taken on raw scores, before scaling (scale > 0).
+    auto softmax = [&](f32x16 (&sacc)[2], uint4 (&pf)[4]) -> float {
+        // max as a tree (short dependency chains)
+        float mx[4];
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            const int kh = t >> 1, v0 = (t & 1) * 8;
+            mx[t] = fmaxf(fmaxf(fmaxf(sacc[kh][v0], sacc[kh][v0 + 1]), fmaxf(sacc[kh][v0 + 2], sacc[kh][v0 + 3])),
+                          fmaxf(fmaxf(sacc[kh][v0 + 4], sacc[kh][v0 + 5]), fmaxf(sacc[kh][v0 + 6], sacc[kh][v0 + 7])));
+        }
+        float mloc = fmaxf(fmaxf(mx[0], mx[1]), fmaxf(mx[2], mx[3]));
+        // lanes l and l ^ 32 hold the same query: v_permlane32_swap hands
+        // every lane both halves' values (no LDS round trip)
+        {
+            const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mloc), __float_as_uint(mloc), false, false);
+            mloc = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1])) * p.scale_log2;
+        }
+        // lazy rescale: the row's reference max m moves only when a score
+        // exceeds it by more than 2^8 (so p = 2^(s - m) <= 256, exact in
+        // range for bf16 P and fp32 sums); the wave skips the O rescale
+        // when no row moved. O / l is unchanged: both carry the same m.
+        const bool move = mloc > m + 8.0f;
+        const float mnew = move ? mloc : m;
+        const float msub = mnew == -INFINITY ? 0.0f : mnew;
+        const float alpha = move ? __builtin_amdgcn_exp2f(m - msub) : 1.0f;
+        float ls[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            const int kh = c >> 1, vb = (c & 1) * 8;
+            float pv[8];
 #pragma unroll
             for (int e = 0; e < 8; ++e) {
-                const int d = c * 8 + e;
-                // the 16-bit halves e&1 of keys (0, 1) and (2, 3), paired by
-                // one byte permute each: v_perm_b32(hi, lo, sel) picks bytes
-                // of the 64-bit {hi, lo}, sel 0x05040100 = low halves,
-                // 0x07060302 = high halves
-                const uint32_t sel = (e & 1) ? 0x07060302u : 0x05040100u;
-                *reinterpret_cast<uint2 *>(&Vt[b][d * kKvBlk + (((u >> 1) ^ VSwz(d)) * 8) + (u & 1) * 4]) =
-                    make_uint2(__builtin_amdgcn_perm(w1[e >> 1], w0[e >> 1], sel),
-                               __builtin_amdgcn_perm(w3[e >> 1], w2[e >> 1], sel));
+                pv[e] = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[kh][vb + e], p.scale_log2, -msub));
+                ls[e & 3] += pv[e];
+            }
+            pf[c] = make_uint4(Pack2<DT>(pv[0], pv[1]), Pack2<DT>(pv[2], pv[3]), Pack2<DT>(pv[4], pv[5]),
+                               Pack2<DT>(pv[6], pv[7]));
+        }
+        l = l * alpha + ((ls[0] + ls[1]) + (ls[2] + ls[3]));
+        m = mnew;
+        return (__builtin_amdgcn_read_exec() & __ballot(move)) != 0 ? alpha : 1.0f;
+    };
+    // O^T += V^T . P^T of one block
+    auto pv = [&](const uint16_t *V, const uint4 (&pf)[4]) {
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+#pragma unroll
+            for (int b = 0; b < DBLK; ++b) {
+                const AttnS4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                    (LdsS4)(const_cast<uint16_t *>(V) + c * 16 * D + vaddr[b]));
+                const AttnS4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                    (LdsS4)(const_cast<uint16_t *>(V) + (c * 16 + 8) * D + vaddr[b]));
+                // whole-vector casts: element swizzles of the read's result
+                // (lo.zw) have been lowered as copies of its low dword
+                const AttnU2 a = __builtin_bit_cast(AttnU2, lo), z = __builtin_bit_cast(AttnU2, hi);
+                oacc[b] = Mfma<DT>(make_uint4(a.x, a.y, z.x, z.y), pf[c], oacc[b]);
             }
         }
     };
-
-    load(kb_lo);
-    store(0);
-    __syncthreads();
-
-    for (int kb = kb_lo; kb < kb_hi; ++kb) {
-        const int kv0 = kb * kKvBlk;
-        const int cur = (kb - kb_lo) & 1;
-        const bool more = kb + 1 < kb_hi;
-        if (more) load(kb + 1);
-
-        if (kv0 <= wave_q_hi) {  // else: block entirely in this wave's future
-            const uint16_t *K = Ks[cur];
-            const uint16_t *V = Vt[cur];
-            f32x16 sacc[2];
+    auto rescale = [&](float alpha) {
+        if (__builtin_expect(__ballot(alpha != 1.0f) != 0, 0)) {
 #pragma unroll
-            for (int kh = 0; kh < 2; ++kh) {
+            for (int b = 0; b < DBLK; ++b)
 #pragma unroll
-                for (int v = 0; v < 16; ++v) sacc[kh][v] = 0.0f;
-                const int r = kh * 32 + (lane & 31);
-#pragma unroll
-                for (int dc = 0; dc < D / 16; ++dc) {
-                    const uint4 kf = *reinterpret_cast<const uint4 *>(K + r * D + KSwz<D>(r, dc * 2 + hf) * 8);
-                    sacc[kh] = Mfma<DT>(kf, qf[dc], sacc[kh]);
-                }
-            }
-
-            // raw scores: the row max is taken before scaling (scale > 0);
-            // masked keys (above the diagonal, past S) by select, not branch
-            float mloc = -INFINITY;
-            const bool diag = kv0 + kKvBlk - 1 > q0 + wave * 32 || kv0 + kKvBlk > p.S;
-            if (diag) {
-#pragma unroll
-                for (int kh = 0; kh < 2; ++kh)
-#pragma unroll
-                    for (int v = 0; v < 16; ++v) {
-                        const int kv = kv0 + kh * 32 + 8 * (v >> 2) + 4 * hf + (v & 3);
-                        sacc[kh][v] = kv > qrow || kv >= p.S ? -INFINITY : sacc[kh][v];
-                    }
-            }
-#pragma unroll
-            for (int kh = 0; kh < 2; ++kh)
-#pragma unroll
-                for (int v = 0; v < 16; ++v) mloc = fmaxf(mloc, sacc[kh][v]);
-            mloc = fmaxf(mloc, __shfl_xor(mloc, 32, 64)) * p.scale_log2;
-            // lazy rescale: the row's reference max m moves only when a score
-            // exceeds it by more than 2^8 (so p = 2^(s - m) <= 256, exact in
-            // range for bf16 P and fp32 sums); the wave skips the O rescale
-            // when no row moved. O / l is unchanged: both carry the same m.
-            const bool move = mloc > m + 8.0f;
-            const float mnew = move ? mloc : m;
-            const float msub = mnew == -INFINITY ? 0.0f : mnew;
-            const float alpha = move ? __builtin_amdgcn_exp2f(m - msub) : 1.0f;
-            float lsum = 0.0f;
-#pragma unroll
-            for (int kh = 0; kh < 2; ++kh)
-#pragma unroll
-                for (int v = 0; v < 16; ++v) {
-                    const float pv = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[kh][v], p.scale_log2, -msub));
-                    sacc[kh][v] = pv;
-                    lsum += pv;
-                }
-            l = l * alpha + lsum;
-            m = mnew;
-            if (__builtin_expect((__builtin_amdgcn_read_exec() & __ballot(move)) != 0, 0)) {
-#pragma unroll
-                for (int b = 0; b < DBLK; ++b)
-#pragma unroll
-                    for (int v = 0; v < 16; ++v) oacc[b][v] *= alpha;
-            }
-
-#pragma unroll
-            for (int c = 0; c < 4; ++c) {
-                const int kh = c >> 1;
-                const int vb = (c & 1) * 8;
-                uint32_t pw[4];
-#pragma unroll
-                for (int s = 0; s < 4; ++s) pw[s] = Pack2<DT>(sacc[kh][vb + 2 * s], sacc[kh][vb + 2 * s + 1]);
-                const uint4 pf = make_uint4(pw[0], pw[1], pw[2], pw[3]);
-#pragma unroll
-                for (int b = 0; b < DBLK; ++b) {
-                    const int d = b * 32 + (lane & 31);
-                    const uint4 vf = *reinterpret_cast<const uint4 *>(V + d * kKvBlk + (((2 * c + hf) ^ VSwz(d)) * 8));
-                    oacc[b] = Mfma<DT>(vf, pf, oacc[b]);
-                }
-            }
+                for (int v = 0; v < 16; ++v) oacc[b][v] *= alpha;
         }
-        if (more) store(cur ^ 1);  // the other buffer was last read before the previous barrier
+    };
+
+    // Stage s: this half's block kb_lo + s*KH + hv; K and V of stage s+1 are
+    // fetched into the other ring slot while stage s is computed.
+    const int kb_lo = item.kb_lo, kb_hi = item.kb_hi;
+    const int ns = (kb_hi - kb_lo + KH - 1) / KH;
+    dma(p.k, p.ldk, koff, kring0, kb_lo + hv, 0, false);
+    dma(p.v, p.ldv, voff, vring0, kb_lo + hv, 0, true);
+    KR_WAIT_VM(0);
+    __syncthreads();
+    for (int st = 0; st < ns; ++st) {
+        const int kb = kb_lo + st * KH + hv;
+        if (st + 1 < ns) {  // the other slot was last read before the previous barrier
+            dma(p.k, p.ldk, koff, kring0, kb + KH, (st + 1) & 1, false);
+            dma(p.v, p.ldv, voff, vring0, kb + KH, (st + 1) & 1, true);
+        }
+        // else: the block is past this item's range (odd block count) or
+        // entirely in this wave's future
+        if (kb < kb_hi && kb * kKvBlk <= wave_q_hi) {
+            f32x16 sacc[2];
+            qk(kring[st & 1][hv], sacc);
+            mask(sacc, kb * kKvBlk);
+            uint4 pf[4];
+            rescale(softmax(sacc, pf));
+            pv(vring[st & 1][hv], pf);
+        }
+        KR_WAIT_VM(0);  // this wave's DMA of the next stage has landed
         __syncthreads();
+    }
+
+    if constexpr (KH == 2) {
+        // waves 4..7 hand their (O, m, l) to waves 0..3 of the same queries
+        // through the rings (free: the loop ended on a barrier), lane-major
+        // so that a wave's 64 lanes touch 64 consecutive words
+        constexpr int NE = DBLK * 16;
+        static_assert(4 * NE * 64 * 4 <= int(sizeof(kring)) && 4 * 2 * 64 * 4 <= int(sizeof(vring)), "merge area");
+        float *mg = reinterpret_cast<float *>(&kring[0][0][0]) + wave * NE * 64 + lane;
+        float *ml = reinterpret_cast<float *>(&vring[0][0][0]) + wave * 2 * 64 + lane;
+        if (hv == 1) {
+#pragma unroll
+            for (int b = 0; b < DBLK; ++b)
+#pragma unroll
+                for (int v = 0; v < 16; ++v) mg[(b * 16 + v) * 64] = oacc[b][v];
+            ml[0] = m;
+            ml[64] = l;
+        }
+        __syncthreads();
+        if (hv == 0) {
+            const float m1 = ml[0];
+            const float mn = fmaxf(m, m1);
+            const float ms = mn == -INFINITY ? 0.0f : mn;
+            const float a0 = __builtin_amdgcn_exp2f(m - ms), a1 = __builtin_amdgcn_exp2f(m1 - ms);
+            l = __builtin_fmaf(ml[64], a1, l * a0);
+#pragma unroll
+            for (int b = 0; b < DBLK; ++b)
+#pragma unroll
+                for (int v = 0; v < 16; ++v) oacc[b][v] = __builtin_fmaf(mg[(b * 16 + v) * 64], a1, oacc[b][v] * a0);
+            m = mn;
+        }
     }
 
     if (item.pieces > 1) {
@@ -329,24 +429,31 @@ __global__ void __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_wav
         auto part = [&](int piece, int ch, int e) {
             return p.ws + (((slot0 + piece) * NCH + ch) * 256 + tid) * 4 + e;
         };
+        if (hv == 0) {
 #pragma unroll
-        for (int b = 0; b < DBLK; ++b)
+            for (int b = 0; b < DBLK; ++b)
 #pragma unroll
-            for (int v = 0; v < 16; ++v)
-                __hip_atomic_store(part(item.piece, b * 4 + v / 4, v % 4), oacc[b][v], __ATOMIC_RELAXED,
-                                   __HIP_MEMORY_SCOPE_AGENT);
-        __hip_atomic_store(part(item.piece, NCH - 1, 0), m, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        __hip_atomic_store(part(item.piece, NCH - 1, 1), l, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this thread's partial is written
+                for (int v = 0; v < 16; ++v)
+                    __hip_atomic_store(part(item.piece, b * 4 + v / 4, v % 4), oacc[b][v], __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(part(item.piece, NCH - 1, 0), m, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(part(item.piece, NCH - 1, 1), l, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this thread's partial is written
+        }
         __syncthreads();
-        if (tid == 0) {
+        if (threadIdx.x == 0) {
             int32_t *c = p.cnt + int64_t(item.sid) * p.HQ + h;
             const int32_t t = __hip_atomic_fetch_add(c, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             last_piece = t == item.pieces - 1;
             if (last_piece) __hip_atomic_store(c, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
         __syncthreads();
-        if (!last_piece) return;
+        if (!last_piece) return;  // the whole workgroup leaves together
+        // the partials were stored at agent scope (device-coherent) before
+        // the other pieces' tickets; acquire at agent scope so no stale line
+        // of this CU's caches serves the reads below
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+        if (hv != 0) return;  // no barrier follows
         float mp[4], lp[4];
         float mall = -INFINITY;
         for (int q = 0; q < item.pieces; ++q) {
@@ -372,6 +479,7 @@ __global__ void __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_wav
                         oacc[b][v]);
         }
     }
+    if (hv != 0) return;
     l += __shfl_xor(l, 32, 64);
     const float inv = l > 0.0f ? 1.0f / l : 0.0f;
     if (qrow < p.S) {
@@ -436,16 +544,80 @@ AttnPlan PlanAttn(int S, bool split)
 
 }  // namespace
 
-// Resident workgroup slots of the device (two 256-thread workgroups per CU).
-int AttnSlots()
+namespace {
+
+// KR_ATTN_KH: 1 or 2 forces the key halves per workgroup; 0 (default) picks
+int AttnKhEnv()
+{
+    static const int v = [] {
+        const char *e = std::getenv("KR_ATTN_KH");
+        const int k = e != nullptr ? std::atoi(e) : 0;
+        return k == 1 || k == 2 ? k : 0;
+    }();
+    return v;
+}
+
+template <int DT, int D, int KH>
+const void *AttnFn()
+{
+    return reinterpret_cast<const void *>(&AttnKernel<DT, D, KH>);
+}
+
+const void *AttnKernelFor(int dtype, int D, int kh)
+{
+    const bool bf = dtype == kBF16;
+    if (D == 128) {
+        if (kh == 2) return bf ? AttnFn<kBF16, 128, 2>() : AttnFn<kF16, 128, 2>();
+        return bf ? AttnFn<kBF16, 128, 1>() : AttnFn<kF16, 128, 1>();
+    }
+    if (kh == 2) return bf ? AttnFn<kBF16, 64, 2>() : AttnFn<kF16, 64, 2>();
+    return bf ? AttnFn<kBF16, 64, 1>() : AttnFn<kF16, 64, 1>();
+}
+
+}  // namespace
+
+int AttnCus()
 {
     static const int v = [] {
         int dev = 0, n = 0;
-        if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+        if (hipGetDevice(&dev) != hipSuccess ||
+            hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n < 1)
             n = 256;
-        return 2 * std::max(n, 1);
+        return n;
     }();
     return v;
+}
+
+// Resident workgroups of the bf16 kernel (head_dim D, kh key halves) on the
+// device: CUs times workgroups per CU, as the runtime's occupancy calculator
+// gives them (the LDS rings of the 8-wave kernel at D 128 leave room for one
+// per CU, the 4-wave kernel's for two).
+int AttnSlots(int D, int kh)
+{
+    static int cache[2][2] = {{0, 0}, {0, 0}};
+    int &v = cache[D == 128 ? 1 : 0][kh - 1];
+    if (v == 0) {
+        int per = 0;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, AttnKernelFor(kBF16, D, kh), 256 * kh, 0) != hipSuccess ||
+            per < 1)
+            per = kh == 1 ? 2 : 1;
+        v = AttnCus() * per;
+    }
+    return v;
+}
+
+// Key halves: 2 (8 waves; the longest causal row walked in half the stages,
+// one workgroup per CU) while the 4-wave grid fits the device's resident
+// slots in one round, so that its longest rows would set the time; 1 (4
+// waves, two independent workgroups per CU) for larger grids, which the
+// heaviest-first order balances on its own. Measured on MI355X, causal,
+// D 128: 2048 x 28 heads 61 (kh 2) vs 67 us (kh 1); 4096 x 32 heads 193
+// vs 177 us.
+int AttnKh(int S, int HQ, int D)
+{
+    if (AttnKhEnv() != 0) return AttnKhEnv();
+    const int64_t grid = int64_t((S + kQBlk - 1) / kQBlk) * HQ;
+    return grid <= AttnSlots(D, 1) ? 2 : 1;
 }
 
 void AttnSplitNeeds(int S, int HQ, int D, size_t *ws_bytes, int *counters)
@@ -453,11 +625,17 @@ void AttnSplitNeeds(int S, int HQ, int D, size_t *ws_bytes, int *counters)
     *ws_bytes = 0;
     *counters = 0;
     if (S <= 0 || HQ <= 0 || (D != 64 && D != 128)) return;
-    // Split only a grid that leaves half the resident slots empty: a fuller
-    // grid is bound by the CUs' MFMA, softmax and LDS throughput, not by its
-    // longest row (measured on MI355X: 28 heads at S=2048 94 -> 116 us split,
-    // 14 heads 59 -> 49 us).
-    if (int64_t((S + kQBlk - 1) / kQBlk) * HQ * 2 > AttnSlots()) return;
+    // Split only a grid of at most half as many workgroups as CUs: a fuller
+    // grid is bound by the CUs' throughput, not by its longest row, and the
+    // 8-wave kernel already halves that row (measured on MI355X, causal:
+    // 2048 x 28 heads D 128 60 us unsplit vs 61 split, 2048 x 14 heads D 64
+    // 37 vs 52, 4096 x 32 heads D 128 180 vs 196).
+    // KR_ATTN_SPLIT=1 splits whatever the grid (for timing the policy).
+    static const bool force = [] {
+        const char *e = std::getenv("KR_ATTN_SPLIT");
+        return e != nullptr && std::atoi(e) == 1;
+    }();
+    if (!force && int64_t((S + kQBlk - 1) / kQBlk) * HQ * 2 > AttnCus()) return;
     const AttnPlan pl = PlanAttn(S, true);
     if (pl.nsplit == 0 || pl.items.size() > size_t(kMaxItems)) return;
     *ws_bytes = size_t(pl.nsplit) * HQ * pl.pmax * (D / 32 * 4 + 1) * 256 * 16;
@@ -501,18 +679,23 @@ void AttnLaunch(int dtype, const void *q, int64_t ldq, const void *k, int64_t ld
     p.ws = use_split ? split->ws : nullptr;
     p.cnt = use_split ? split->cnt : nullptr;
     p.pmax = pl.pmax;
-    const dim3 grid(unsigned(pl.items.size()) * unsigned(HQ));
-    const bool bf = dtype == kBF16;
+    // XCD-aware order where the kv heads share out evenly over 8 XCDs
+    // (KR_ATTN_XCD=0 keeps the plain order)
+    static const bool xcd_off = [] {
+        const char *e = std::getenv("KR_ATTN_XCD");
+        return e != nullptr && std::atoi(e) == 0;
+    }();
+    const int nit = int(pl.items.size());
+    p.nitems = nit;
+    p.xcds = !xcd_off && (8 % HKV == 0 || HKV % 8 == 0) ? 8 : 0;
+    unsigned nwg = unsigned(nit) * unsigned(HQ);
+    if (p.xcds != 0) nwg = 8u * unsigned((int64_t(nit) * HQ + 7) / 8);
+    const dim3 grid(nwg);
     if (dtype != kBF16 && dtype != kF16) throw std::runtime_error("attention: dtype must be bf16 or f16");
-    if (D == 128) {
-        if (bf) hipLaunchKernelGGL((AttnKernel<kBF16, 128>), grid, dim3(256), 0, stream, p);
-        else hipLaunchKernelGGL((AttnKernel<kF16, 128>), grid, dim3(256), 0, stream, p);
-    } else if (D == 64) {
-        if (bf) hipLaunchKernelGGL((AttnKernel<kBF16, 64>), grid, dim3(256), 0, stream, p);
-        else hipLaunchKernelGGL((AttnKernel<kF16, 64>), grid, dim3(256), 0, stream, p);
-    } else {
-        throw std::runtime_error("attention: head_dim must be 64 or 128");
-    }
+    if (D != 128 && D != 64) throw std::runtime_error("attention: head_dim must be 64 or 128");
+    const int kh = AttnKh(S, HQ, D);
+    void *args[] = {&p};
+    Check(hipLaunchKernel(AttnKernelFor(dtype, D, kh), grid, dim3(256 * kh), args, 0, stream), "attention launch");
     Check(hipGetLastError(), "attention launch");
 }
 

@@ -23,6 +23,7 @@
 //   (8-byte writes, XOR-swizzled) and leaves as full-line 16-byte stores. Then
 //   the workgroup arrives on its row tile's relay counter; the last arrival
 //   releases the tile.
+#include "kr_dma.h"
 #include "kr_gemm.h"
 #include "kr_relay.h"
 #include "kr_rowcore.h"
