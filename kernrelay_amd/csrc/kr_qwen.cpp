@@ -814,10 +814,12 @@ private:
     // override both. Measured on MI355X, a static CU partition for the
     // consumer costs every producer kernel its CUs (5.5% of the prefill for 2
     // CUs per XCD), and consumer workgroups interleaved onto the producer's
-    // CUs starve 256x256 GEMM workgroups, which need a whole CU. Edges behind
-    // single-round producers (o, down -> Add+RMSNorm) release all their tiles
-    // at once, so they stay in stream order. Every row goes through the same
-    // arithmetic as in the serial schedule: identical bits.
+    // CUs starve 256x256 GEMM workgroups, which need a whole CU. The o and
+    // down GEMMs (single-round producers at these shapes) release their k row
+    // tiles through device flags, and the Add+RMSNorm of each released tile
+    // runs in the GEMM's own workgroups (GemmNormRelay) instead of a kernel
+    // after the GEMM. Every row goes through the same arithmetic as in the
+    // serial schedule: identical bits.
     void BuildSplit()
     {
         const int S = seq_;
