@@ -325,13 +325,21 @@ public:
         relay_grid_ = EnvInt("KR_RELAY_GRID", 256);
         fan_max_ = EnvInt("KR_PLAN_FAN", kMaxFanOut);
         max_spins_ = uint32_t(EnvInt("KR_MAX_SPINS", int(kDefaultMaxSpins)));
-        if (mode_ != "direct" && mode_ != "graph" && mode_ != "graph_per_stream")
-            throw std::runtime_error("mode '" + mode_ + "' is not built (direct, graph, graph_per_stream)");
+        if (mode_ != "direct" && mode_ != "graph" && mode_ != "graph_per_stream" && mode_ != "graph_segment")
+            throw std::runtime_error("mode '" + mode_ +
+                                     "' is not built (direct, graph, graph_per_stream, graph_segment)");
+        // graph_segment joins its graphs with events (the segments' waits and
+        // publishes), whatever KR_SYNC says
+        if (mode_ == "graph_segment") sync_ = "event";
     }
 
     ~Executor()
     {
         for (auto &g : graphs_) {
+            if (g.exec) (void)hipGraphExecDestroy(g.exec);
+            if (g.graph) (void)hipGraphDestroy(g.graph);
+        }
+        for (auto &g : segments_) {
             if (g.exec) (void)hipGraphExecDestroy(g.exec);
             if (g.graph) (void)hipGraphDestroy(g.graph);
         }
@@ -381,6 +389,8 @@ public:
             Check(hipStreamWaitEvent(streams_.cons, ev0_, 0), "consumer start");
             if (mode_ == "direct") {
                 EnqueueRank(r);
+            } else if (mode_ == "graph_segment") {
+                RunSegments(r);
             } else {
                 for (auto &g : graphs_)
                     if (g.rank == r) Check(hipGraphLaunch(g.exec, g.lane == 0 ? streams_.prod : streams_.cons), "graph launch");
@@ -1010,7 +1020,9 @@ private:
         }
     }
 
-    void EnqueueTask(RankCtx &rc, Launch &L, hipStream_t s)
+    // events = false: leave the launch's event waits and records to the
+    // caller (graph_segment puts them between its graphs)
+    void EnqueueTask(RankCtx &rc, Launch &L, hipStream_t s, bool events = true)
     {
         const NodeSpec &n = *L.node;
         const TaskSpec &t = *L.task;
@@ -1019,7 +1031,7 @@ private:
         const int64_t in_rows = TaskRows(t);
         const int64_t out_off = TaskOutOff(t);
 
-        if (sync_ == "event") {
+        if (sync_ == "event" && events) {
             for (hipEvent_t e : L.wait_events) Check(hipStreamWaitEvent(s, e, 0), "stream wait event");
         }
         for (const auto &w : L.extra_waits) WaitLaunch(w, 0, 1, s);
@@ -1080,7 +1092,7 @@ private:
             }
         }
         Check(hipGetLastError(), "task launch");
-        if (L.publish && sync_ == "event") Check(hipEventRecord(L.pub_event, s), "record event");
+        if (L.publish && sync_ == "event" && events) Check(hipEventRecord(L.pub_event, s), "record event");
     }
 
     void EnqueueRank(int r)
@@ -1091,8 +1103,85 @@ private:
         }
     }
 
+    // graph_segment (the reference's NHP_GRAPH_SEGMENT, exec_main.cpp:
+    // 1150-1273): each stream's launches are cut into runs, a run ending
+    // after a launch that publishes and a new one starting at a launch that
+    // waits on an event; each run is captured as one graph. A run's waits
+    // are its first launch's, its publishes its last launch's.
+    void CaptureSegments()
+    {
+        for (int r = 0; r < doc_.nranks; ++r)
+            for (int lane = 0; lane < 2; ++lane) {
+                std::vector<size_t> run;
+                auto close = [&]() {
+                    if (run.empty()) return;
+                    Segment g{};
+                    g.rank = r;
+                    g.lane = lane;
+                    g.waits = launches_[run.front()].wait_events;
+                    for (size_t i : run)
+                        if (launches_[i].publish) g.pubs.push_back(launches_[i].pub_event);
+                    hipStream_t s = StreamOf(lane);
+                    Check(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal), "begin capture");
+                    for (size_t i : run) EnqueueTask(ranks_[r], launches_[i], s, false);
+                    Check(hipStreamEndCapture(s, &g.graph), "end capture");
+                    Check(hipGraphInstantiate(&g.exec, g.graph, nullptr, nullptr, 0), "instantiate");
+                    segments_.push_back(g);
+                    run.clear();
+                };
+                for (size_t idx : enqueue_order_) {
+                    const Launch &L = launches_[idx];
+                    if (L.lane != lane) continue;
+                    if (!run.empty() && !L.wait_events.empty()) close();
+                    run.push_back(idx);
+                    if (L.publish) close();
+                }
+                close();
+            }
+    }
+
+    // Launch rank r's segments in dependency order: a segment goes out once
+    // every event it waits on has been recorded in this run, behind
+    // hipStreamWaitEvent on them; its publishes are recorded right after it.
+    void RunSegments(int r)
+    {
+        std::set<hipEvent_t> recorded;
+        std::vector<char> done(segments_.size(), 0);
+        size_t remaining = 0;
+        for (const auto &g : segments_) remaining += g.rank == r;
+        while (remaining > 0) {
+            bool progress = false;
+            for (size_t i = 0; i < segments_.size(); ++i) {
+                Segment &g = segments_[i];
+                if (g.rank != r || done[i]) continue;
+                bool ready = true;
+                for (hipEvent_t e : g.waits)
+                    if (recorded.count(e) == 0) {
+                        ready = false;
+                        break;
+                    }
+                if (!ready) continue;
+                hipStream_t s = StreamOf(g.lane);
+                for (hipEvent_t e : g.waits) Check(hipStreamWaitEvent(s, e, 0), "segment wait");
+                Check(hipGraphLaunch(g.exec, s), "segment launch");
+                for (hipEvent_t e : g.pubs) {
+                    Check(hipEventRecord(e, s), "segment record");
+                    recorded.insert(e);
+                }
+                done[i] = 1;
+                --remaining;
+                progress = true;
+            }
+            if (!progress) throw std::runtime_error("segment wait cycle");
+        }
+    }
+
     void Capture()
     {
+        if (mode_ == "graph_segment") {
+            CaptureSegments();
+            return;
+        }
         for (int r = 0; r < doc_.nranks; ++r) {
             if (sync_ == "event") {
                 // one multi-stream graph: fork the consumer stream off the producer
@@ -1141,6 +1230,15 @@ private:
         int lane;
         int rank;
     };
+    struct Segment {
+        hipGraph_t graph;
+        hipGraphExec_t exec;
+        int lane;
+        int rank;
+        std::vector<hipEvent_t> waits;
+        std::vector<hipEvent_t> pubs;
+    };
+    std::vector<Segment> segments_;
 
     SchedDoc doc_;
     int device_;

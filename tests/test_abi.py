@@ -93,5 +93,5 @@ def test_unknown_op_and_mode_rejected(tmp_path):
     bad["nodes"][1]["op"] = "topk"
     proc = run_plan_subprocess(schedule.dump_schedule(bad, tmp_path / "topk.json"))
     assert "RC 1" in proc.stdout and "not built" in proc.stderr
-    proc = run_plan_subprocess(schedule.dump_schedule(sched, tmp_path / "ok.json"), mode="graph_segment")
+    proc = run_plan_subprocess(schedule.dump_schedule(sched, tmp_path / "ok.json"), mode="graph_bogus")
     assert "RC 1" in proc.stdout and "not built" in proc.stderr

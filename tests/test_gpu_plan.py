@@ -86,6 +86,35 @@ def test_event_sync_matches_flags(gpu, tmp_path):
             assert np.array_equal(flag[k], ev[k])
 
 
+@pytest.mark.parametrize("chunking", [{"mm": 2, "gelu": 2}, {"mm": 4, "gelu": 2}, {"mm": 1, "gelu": 4}])
+def test_graph_segment_matches_flags(gpu, tmp_path, chunking):
+    """graph_segment (the reference's NHP_GRAPH_SEGMENT): each stream's tasks
+    cut into graphs at every cross-stream wait and after every publish, joined
+    by events; the outputs equal the flag relay's bit for bit, repeated runs
+    included."""
+    dag = workloads.tiny_mm_gelu(tmp_path)
+    sched = schedule.build_fixed_schedule(dag, chunking)
+    _, flag = run(sched, tmp_path, "flag")
+    r, seg = run(sched, tmp_path, "segment", mode="graph_segment", iters=3, warmup=1)
+    assert r["ok"] and r["sync"] == "event" and r["mode"] == "graph_segment"
+    for k in flag:
+        assert np.array_equal(flag[k], seg[k]), k
+
+
+@pytest.mark.parametrize("name,consumers,expected", KATS[:2])
+def test_graph_segment_reference_checksums(gpu, tmp_path, name, consumers, expected):
+    """The reference's KAT DAGs (2 ranks, split at k=4) in graph_segment mode
+    reproduce its recorded checksums."""
+    dag = kat_dag(name, consumers)
+    sched = schedule.build_fixed_schedule(dag, {n.name: 4 for n in dag.nodes}, nranks=2)
+    path = schedule.dump_schedule(sched, tmp_path / "kat_seg.json")
+    announce("plan_run KAT graph_segment " + name)
+    r = libapi.plan_run(path, devices="0,0", mode="graph_segment", iters=2, warmup=1,
+                        out_json=tmp_path / "kat_seg_out.json")
+    assert r["_rc"] == 0 and r["ok"], r
+    assert abs(r["checksum"] - expected) / abs(expected) < 1e-3, (r["checksum"], expected)
+
+
 def test_wait_kernel_variant_matches(gpu, tmp_path):
     dag = workloads.tiny_mm_gelu(tmp_path)
     sched = schedule.build_fixed_schedule(dag, {"mm": 2, "gelu": 2})
