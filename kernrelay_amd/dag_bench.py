@@ -5,7 +5,9 @@
 * fan-out: X[4096,4096] . W[4096,4096] -> {row softmax, GELU, bf16->fp16
   cast} per row tile, serial (one stream), B0 (two streams, unsplit) and the
   relay split at k = 1, 2, 4, 8 (schedules from kernrelay_amd.schedule, as
-  the reference's E3/E4 variants, python/kernrelay/e34.py:16-22).
+  the reference's E3/E4 variants, python/kernrelay/e34.py:16-22);
+* the reference's own relay cases (fp16 32768x1024x2048 GEMM -> GELU,
+  softmax, cast, {GELU, softmax}) at its k, next to its published times.
 
 Each variant runs as a replayed graph per stream (`graph_per_stream`); the
 reported time is the device makespan (HIP events on both streams, best and
@@ -96,6 +98,40 @@ def tiny(tmp, iters=50, warmup=5):
             "checksums_equal": serial["checksum"] == split["checksum"]}
 
 
+# The reference's relay table (Ascend 910B3, nhp_exec, best of 3 x 5 runs):
+# case -> (consumers, k, serial us, B0 us, split us), RESULTS.md:67-76.
+E34_REFERENCE = {
+    "mm_gelu_k2": (["gelu"], 2, 971.7, 981.1, 890.4),
+    "mm_gelu_k4": (["gelu"], 4, 978.8, 974.0, 889.2),
+    "mm_gelu_k8": (["gelu"], 8, 1008.4, 1014.9, 911.3),
+    "mm_softmax_k4": (["softmax"], 4, 1133.0, 1132.3, 888.4),
+    "mm_cast_k4": (["cast"], 4, 1018.6, 966.3, 944.2),
+    "mm_fanout_gelu_softmax_k4": (["gelu", "softmax"], 4, 1406.1, 1424.5, 1318.3),
+}
+
+
+def reference_e34(tmp, iters=20, warmup=3):
+    """The reference's own relay cases at its shapes and dtype (fp16 GEMM
+    32768x1024x2048 -> consumers, DetValue inputs, one rank): serial, B0 and
+    the split at the reference's k, with the reference's published times
+    beside ours."""
+    out = {}
+    for case, (consumers, k, r_serial, r_b0, r_split) in E34_REFERENCE.items():
+        dag = workloads.e34_dag(case, consumers)
+        v = workloads.variants(dag, k)
+        rs = {name: _plan(v[name], tmp, "%s_%s" % (case, name), iters, warmup) for name in ("serial", "b0", "split")}
+        ours = {name: round(rs[name]["device_best_us"], 2) for name in rs}
+        out[case] = {
+            "k": k,
+            "serial_us": ours["serial"], "b0_us": ours["b0"], "split_us": ours["split"],
+            "serial_over_split": round(ours["serial"] / ours["split"], 4),
+            "reference_serial_over_split": round(r_serial / r_split, 4),
+            "reference_us": {"serial": r_serial, "b0": r_b0, "split": r_split},
+            "checksums_equal": len({rs[n]["checksum"] for n in rs}) == 1,
+        }
+    return out
+
+
 def _event_us(fn, reps=10):
     import torch
     fn()
@@ -138,7 +174,7 @@ def kernels_alone(M=4096, K=4096, N=4096):
 def run_all(iters=20):
     with tempfile.TemporaryDirectory(prefix="kr_dag_") as tmp:
         return {"tiny_mm_gelu": tiny(tmp), "fanout_4096": fanout(tmp, iters=iters),
-                "alone_4096": kernels_alone()}
+                "alone_4096": kernels_alone(), "reference_e34": reference_e34(tmp, iters=iters)}
 
 
 def main(argv=None):

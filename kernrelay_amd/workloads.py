@@ -6,7 +6,8 @@ seeded input files for kr_plan_run.
   dags/e0_tiny_mm_gelu.json, at the task's shapes and dtype);
 * mm fan-out: X[4096,4096] ~ N(0,1), W[4096,4096] ~ N(0,0.02), bf16; every
   tile feeds row-softmax, GELU and a bf16->fp16 cast (the reference's 1:N
-  fan-out, dags/f04_mm_fanout_c2.json, with the cast consumer added).
+  fan-out, dags/f04_mm_fanout_c2.json, with the cast consumer added);
+* the reference's own E3/E4 DAGs at their shapes and dtype (`e34_dag`).
 
 Inputs are written once per (shape, seed) as raw bf16 files: X as [M, K],
 W as the weight_t layout [K, N] the executor reads.
@@ -54,6 +55,28 @@ def tiny_mm_gelu(out_dir, seed=1234):
 def mm_fanout(out_dir, M=4096, K=4096, N=4096, seed=1234, consumers=("softmax", "gelu", "cast")):
     inputs = write_inputs(out_dir, M, K, N, seed)
     return schedule.dag_from_dict(mm_consumers_dag("mm_fanout", M, K, N, list(consumers), inputs=inputs))
+
+
+def e34_dag(name, consumers, M=32768, K=1024, N=2048):
+    """The reference's E3/E4 relay DAGs (dags/f01_mm_gelu_c2.json,
+    e3_mm_softmax.json, e3_mm_cast.json, f04_mm_fanout_c2.json): one fp16
+    GEMM X[32768,1024] . W[1024,2048] feeding each consumer, deterministic
+    inputs (the executor's DetValue), 4 tiles by default. `consumers` None:
+    the reverse edge of dags/e3_ln_mm.json, a LayerNorm [32768, 2048]
+    producer feeding a GEMM with K = N = 2048."""
+    if consumers is None:
+        return schedule.dag_from_dict({"name": name, "nodes": [
+            {"name": "ln", "op": "layernorm", "engine": "aiv", "shape": {"rows": M, "cols": 2048},
+             "dtype": "fp16", "tiles": 4},
+            {"name": "mm", "op": "matmul", "engine": "aic", "shape": {"M": M, "K": 2048, "N": 2048},
+             "dtype": "fp16", "tiles": 4}], "edges": [{"src": "ln", "dst": "mm", "kind": "data"}]})
+    nodes = [{"name": "mm", "op": "matmul", "engine": "aic", "shape": {"M": M, "K": K, "N": N},
+              "dtype": "fp16", "tiles": 4}]
+    for c in consumers:
+        nodes.append({"name": c, "op": c, "engine": "aiv", "shape": {"rows": M, "cols": N},
+                      "dtype": "fp16", "tiles": 4})
+    edges = [{"src": "mm", "dst": c, "kind": "data"} for c in consumers]
+    return schedule.dag_from_dict({"name": name, "nodes": nodes, "edges": edges})
 
 
 def variants(dag, k, nranks=1):

@@ -261,8 +261,11 @@ def test_embedding(gpu):
 
 
 @pytest.mark.parametrize("S,HQ,HKV,D", [(128, 2, 2, 64), (256, 4, 2, 128), (200, 14, 2, 64), (384, 4, 1, 128),
-                                         (1000, 3, 1, 128), (2048, 28, 4, 128)])
+                                         (1000, 3, 1, 128), (2048, 28, 4, 128), (2048, 64, 8, 128)])
 def test_attention(gpu, S, HQ, HKV, D):
+    """Against the oracle. The grids up to 28 heads at 2048 run the 8-wave
+    key-half kernel; 64 heads at 2048 (1024 workgroups, more than one
+    resident round) the 4-wave kernel."""
     announce("attention S=%d HQ=%d HKV=%d D=%d" % (S, HQ, HKV, D))
     q = rand((S, HQ, D), 1.0, 20)
     k = rand((S, HKV, D), 1.0, 21)

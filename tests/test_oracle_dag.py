@@ -11,20 +11,14 @@ restatement must reproduce them; a wrong seed, input role, row order or op
 import numpy as np
 import pytest
 
-from kernrelay_amd import schedule
+from kernrelay_amd import schedule, workloads
 from oracle import dag_eval, dag_inputs
 
 
 def ref_dag(name, consumers):
     """The reference's dags/f01_mm_gelu_c2.json, e3_mm_softmax.json,
     e3_mm_cast.json and f04_mm_fanout_c2.json shapes (M=32768, K=1024, N=2048, fp16)."""
-    nodes = [{"name": "mm", "op": "matmul", "engine": "aic", "shape": {"M": 32768, "K": 1024, "N": 2048},
-              "dtype": "fp16", "tiles": 4}]
-    for c in consumers:
-        nodes.append({"name": c, "op": c, "engine": "aiv", "shape": {"rows": 32768, "cols": 2048},
-                      "dtype": "fp16", "tiles": 4})
-    edges = [{"src": "mm", "dst": c, "kind": "data"} for c in consumers]
-    return schedule.dag_from_dict({"name": name, "nodes": nodes, "edges": edges})
+    return workloads.e34_dag(name, consumers)
 
 
 KATS = [
@@ -40,11 +34,7 @@ def ln_mm_dag():
     """The reference's dags/e3_ln_mm.json: a LayerNorm producer on the vector
     engine feeding a GEMM consumer (the reverse edge), 32768 x 2048, fp16;
     its recorded checksum is results/final/e34_raw.json:2003 (5.91964)."""
-    return schedule.dag_from_dict({"name": "e3_ln_mm", "nodes": [
-        {"name": "ln", "op": "layernorm", "engine": "aiv", "shape": {"rows": 32768, "cols": 2048},
-         "dtype": "fp16", "tiles": 4},
-        {"name": "mm", "op": "matmul", "engine": "aic", "shape": {"M": 32768, "K": 2048, "N": 2048},
-         "dtype": "fp16", "tiles": 4}], "edges": [{"src": "ln", "dst": "mm", "kind": "data"}]})
+    return workloads.e34_dag("e3_ln_mm", None)
 
 
 def kat_dag(name, consumers):
