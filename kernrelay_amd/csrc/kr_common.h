@@ -129,6 +129,18 @@ __device__ __forceinline__ float RopeSecond(float x2, float x1, float c, float s
 // SiLU as every kernel here computes it (x * sigmoid(x)).
 __device__ __forceinline__ float Silu(float x) { return x * FastRcp(1.0f + FastExp(-x)); }
 
+// GELU, tanh form: 0.5 x (1 + tanh(y)), y = sqrt(2/pi) (x + 0.044715 x^3),
+// computed as the identical x / (1 + e^(-2y)) (1 + tanh(y) = 2 / (1 + e^(-2y))):
+// five full-rate operations and two transcendentals per element. Saturates
+// through the exponential: e^(-2y) -> inf gives -0 for large negative x,
+// -> 0 gives x for large positive x.
+__device__ __forceinline__ float GeluTanh(float x)
+{
+    const float c = -2.0f * 0.7978845608028654f * 1.4426950408889634f;  // -2 sqrt(2/pi) log2(e)
+    const float u = 1.0f + 0.044715f * (x * x);
+    return x * FastRcp(1.0f + __builtin_amdgcn_exp2f(c * x * u));
+}
+
 __device__ __forceinline__ float F16ToF32(uint16_t h)
 {
     _Float16 v;

@@ -35,6 +35,14 @@ struct GemmDesc {
     // rounded as the standalone SwiGLU kernel rounds. C is not written.
     void *epi_act = nullptr;
     int64_t ld_act = 0;
+    // Unary consumer written beside C (the in-register relay of a GEMM to a
+    // GELU / SiLU / cast consumer): y[M, N] (row stride ld_y, dtype y_dtype)
+    // = f(C) for KR_EW_GELU, KR_EW_SILU or KR_EW_CAST, computed from each
+    // stored 16-bit C value exactly as the elementwise kernel computes it.
+    void *y = nullptr;
+    int y_op = 0;
+    int y_dtype = 0;
+    int64_t ld_y = 0;
     // Stream-K (no relay on this launch): when the 256x256 tiles are fewer
     // than the CUs, every CU takes an equal share of the (tile, K stage)
     // iterations and split tiles are summed in piece order by their last

@@ -27,6 +27,7 @@
 #include "kr_gemm.h"
 #include "kr_relay.h"
 #include "kr_rowcore.h"
+#include "kr_rowops.h"
 
 namespace kr {
 
@@ -57,6 +58,9 @@ struct GemmParams {
     int tail_cols;
     uint16_t *epi_act;   // SwiGLU epilogue output [M, N/2] (nullptr: store C)
     int64_t ld_act;
+    void *uy;        // unary consumer output (nullptr: none)
+    int uop, udt;
+    int64_t ldy;
     int sk_wgs;          // stream-K workgroups (0: one tile per workgroup)
     int sk_pmax;         // partial-sum slots per tile in sk_ws
     float *sk_ws;        // [tiles][sk_pmax][BM*BN] fp32 partials
@@ -294,6 +298,70 @@ __device__ void NormTail(const GemmParams &p, int tile, int worker, int workers)
     }
 }
 
+// The unary consumer's pass over the staged tile (after C's): y = f(C) with
+// the elementwise kernel's arithmetic on C's stored values, so y equals what
+// that kernel computes from C bit for bit. Every thread stores 16 bytes of y
+// per step -- 8 values of a 16-bit y, 4 of an fp32 y -- so each store
+// instruction covers whole 128-byte lines (two 16-byte halves of 32-byte
+// runs would leave every line half-written per instruction). Staged chunk c
+// of a row sits in slot c ^ ((row & 31) >> 1), its 8-byte halves swapped on
+// odd rows. Columns past N are not written.
+template <int DT, int BM, int BN, int NT>
+__device__ __forceinline__ void UnaryTile(const GemmParams &p, const uint16_t *stage, int m0, int n0, bool coh)
+{
+    auto f = [&](uint16_t h) {
+        const float x = Elem<DT>::Load(h);
+        return p.uop == kEwGelu ? GeluTanh(x) : (p.uop == kEwSilu ? Silu(x) : x);
+    };
+    if (p.udt == kF32) {
+        constexpr int QPR = BN / 4;  // 4-value quarters per row
+#pragma unroll 4
+        for (int idx = threadIdx.x; idx < BM * QPR; idx += NT) {
+            const int row = idx / QPR;
+            const int q = idx % QPR;
+            const int gm = m0 + row;
+            const int gn = n0 + q * 4;
+            if (gm >= p.M || gn >= p.N) continue;
+            const int slot = (q >> 1) ^ ((row & 31) >> 1);
+            const uint2 u = *reinterpret_cast<const uint2 *>(stage + row * BN + slot * 8 + 4 * ((q ^ row) & 1));
+            const float o[4] = {f(uint16_t(u.x)), f(uint16_t(u.x >> 16)), f(uint16_t(u.y)), f(uint16_t(u.y >> 16))};
+            float *yp = static_cast<float *>(p.uy) + int64_t(gm) * p.ldy + gn;
+            if (gn + 4 <= p.N) {
+                PutU128(yp, make_uint4(__float_as_uint(o[0]), __float_as_uint(o[1]), __float_as_uint(o[2]),
+                                       __float_as_uint(o[3])), coh);
+            } else {
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    if (gn + e < p.N) PutU32(yp + e, __float_as_uint(o[e]), coh);
+            }
+        }
+        return;
+    }
+    constexpr int CPR = BN / 8;
+#pragma unroll 4
+    for (int idx = threadIdx.x; idx < BM * CPR; idx += NT) {
+        const int row = idx / CPR;
+        const int ch = idx % CPR;
+        const int gm = m0 + row;
+        const int gn = n0 + ch * 8;
+        if (gm >= p.M || gn >= p.N) continue;
+        uint4 u = *reinterpret_cast<const uint4 *>(stage + row * BN + (ch ^ ((row & 31) >> 1)) * 8);
+        if (row & 1) u = make_uint4(u.z, u.w, u.x, u.y);
+        U16x8 a, r;
+        *reinterpret_cast<uint4 *>(a.v) = u;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) r.v[e] = p.udt == kBF16 ? Elem<kBF16>::Store(f(a.v[e])) : Elem<kF16>::Store(f(a.v[e]));
+        uint16_t *yp = static_cast<uint16_t *>(p.uy) + int64_t(gm) * p.ldy + gn;
+        if (gn + 8 <= p.N) {
+            PutU128(yp, *reinterpret_cast<const uint4 *>(r.v), coh);
+        } else {
+#pragma unroll
+            for (int e = 0; e < 8; ++e)
+                if (gn + e < p.N) PutU16(yp + e, r.v[e], coh);
+        }
+    }
+}
+
 // Write the workgroup's BMxBN tile of C. acc[i][j] is the C^T block of rows
 // wm*BM/2 + 32i.., cols wn*BN/2 + 32j..: value v of lane l sits at row l%32,
 // col 8*(v/4) + 4*(l/32) + v%4. Each run of 4 columns goes to LDS as one
@@ -396,6 +464,7 @@ __device__ __forceinline__ void StoreTile(const GemmParams &p, f32x16 (&acc)[MI]
                 if (gn + e < p.N) PutU16(dst + e, uint16_t(w[e >> 1] >> ((e & 1) * 16)), coh);
         }
     }
+    if (p.uy != nullptr) UnaryTile<DT, BM, BN, NT>(p, stage, m0, n0, coh);
 }
 
 // SwiGLU epilogue: the in-register relay of the gate/up GEMM to its
@@ -971,6 +1040,20 @@ void GemmLaunch(const GemmDesc &d, hipStream_t stream)
     p.tail_cols = d.tail_cols;
     p.epi_act = static_cast<uint16_t *>(d.epi_act);
     p.ld_act = d.ld_act;
+    p.uy = d.y;
+    p.uop = d.y_op;
+    p.udt = d.y_dtype;
+    p.ldy = d.ld_y > 0 ? d.ld_y : d.N;
+    if (d.y != nullptr) {
+        if (d.y_op != kEwGelu && d.y_op != kEwSilu && d.y_op != kEwCast)
+            throw std::runtime_error("gemm: the unary consumer must be gelu, silu or cast");
+        if (d.y_dtype != kBF16 && d.y_dtype != kF16 && d.y_dtype != kF32)
+            throw std::runtime_error("gemm: unary consumer dtype");
+        if (d.epi_act != nullptr || d.tail_act != nullptr || d.norm_y != nullptr || d.rope_cos != nullptr)
+            throw std::runtime_error("gemm: one epilogue consumer per launch");
+        if ((reinterpret_cast<uintptr_t>(d.y) & 15) != 0 || (p.ldy * int64_t(DTypeBytes(d.y_dtype))) % 16 != 0)
+            throw std::runtime_error("gemm: unary consumer output must be 16-byte aligned rows");
+    }
     if (d.rope_cos != nullptr) {
         if (d.rope_sin == nullptr || (d.rope_d != 64 && d.rope_d != 128) || d.rope_cols <= 0 ||
             d.rope_cols % d.rope_d != 0 || d.rope_cols > d.N || d.rope_pos0 < 0)

@@ -307,6 +307,11 @@ struct Launch {
     // persistent-consumer tiles (those released before the producer GEMM's
     // last round of workgroups); -1 = every tile waits in-kernel
     int early_tiles = -1;
+    // in-register relay (KR_PLAN_EPILOGUE=1): this consumer launch runs in
+    // its producer GEMM's epilogue (skip), or this GEMM launch writes that
+    // consumer's output beside C (epi)
+    bool skip = false;
+    const NodeSpec *epi = nullptr;
 };
 
 struct RankCtx {
@@ -451,6 +456,12 @@ public:
 
     const SchedDoc &doc() const { return doc_; }
     int edges() const { return int(consumed_states_.size()); }
+    int epilogue_consumers() const
+    {
+        int n = 0;
+        for (const auto &L : launches_) n += L.epi != nullptr;
+        return n;
+    }
     const std::string &sync() const { return sync_; }
     int consumer_cus() const { return streams_.cons_cus; }
 
@@ -689,6 +700,45 @@ private:
         return !(best.bm == 256 && best.bn == 256);
     }
 
+    // In-register relay (KR_PLAN_EPILOGUE=1): a GELU / SiLU / cast consumer
+    // that reads every row of one GEMM launch's output, and whose own output
+    // no node reads, is computed in that GEMM's epilogue from each stored C
+    // value with the elementwise kernel's arithmetic (the same bits); its
+    // launch, waits and relay states go away. The tile reaches its consumer
+    // in registers the moment it exists, instead of through HBM after a flag.
+    template <class M>
+    void FuseEpilogues(const M &launch_of)
+    {
+        for (Launch &L : launches_) {
+            if (L.fan.size() != 1) continue;
+            const NodeSpec &C = *L.node;
+            if (C.op != Op::Gelu && C.op != Op::Silu && C.op != Op::Cast) continue;
+            if (C.preds.size() != 1 || L.merged != NodeTiles(C)) continue;
+            const NodeSpec &P = doc_.Node(C.preds[0]);
+            if (P.op != Op::MatMul || C.rows != P.rows || C.cols != P.n) continue;
+            if (TaskInOff(*L.task) != 0 || TaskOutOff(*L.task) != 0 || TaskRows(*L.task) != C.rows) continue;
+            bool read = false;
+            for (const auto &n : doc_.nodes)
+                if (std::find(n.preds.begin(), n.preds.end(), C.id) != n.preds.end()) read = true;
+            if (read) continue;
+            const auto it = launch_of.find({P.id, 0});
+            if (it == launch_of.end()) continue;
+            Launch &PL = launches_[it->second];
+            if (PL.merged != NodeTiles(P) || PL.task->n_tile > 0 || PL.epi != nullptr) continue;
+            if (TaskInOff(*PL.task) != 0 || TaskRows(*PL.task) != P.rows) continue;
+            PL.epi = &C;
+            L.skip = true;
+        }
+        // a producer whose every waiter now runs in its epilogue releases
+        // nothing: it launches like an unreleased GEMM
+        std::set<std::string> awaited;
+        for (const Launch &L : launches_)
+            if (!L.skip)
+                for (const auto &w : L.task->waits) awaited.insert(w.first);
+        for (Launch &L : launches_)
+            if (L.epi != nullptr && !awaited.count(L.node->id)) L.publish = false;
+    }
+
     int EarlyTiles(const Launch &PL, const Launch &L, int64_t in_off, int64_t in_rows) const
     {
         const NodeSpec &P = *PL.node;
@@ -775,6 +825,7 @@ private:
             }
         }
         if (doc_.lanes.size() > 2) throw std::runtime_error("more than two engine lanes after normalization");
+        if (coalesce && EnvInt("KR_PLAN_EPILOGUE", 0) != 0) FuseEpilogues(launch_of);
         // Which tasks are awaited: only cross-lane waits need a flag/event.
         std::map<std::string, int> flag_base;
         int next_block = 0;
@@ -788,6 +839,7 @@ private:
         std::map<std::tuple<std::string, std::string, int>, size_t> last_waiter;
         for (size_t i = 0; i < launches_.size(); ++i) {
             Launch &L = launches_[i];
+            if (L.skip) continue;
             for (const auto &w : L.task->waits) {
                 auto it = launch_of.find(w);
                 if (it == launch_of.end()) throw std::runtime_error("missing plan for task " + w.first);
@@ -818,6 +870,7 @@ private:
             const int64_t in_off = TaskInOff(t);
             const int64_t in_rows = TaskRows(t);
             if (L.publish) L.flag = flag_base.at(n.id) + t.tile;
+            if (L.skip) continue;  // computed in its producer's epilogue
             if (sync_ == "event") {
                 if (L.publish) Check(hipEventCreateWithFlags(&L.pub_event, hipEventDisableTiming), "event");
                 continue;
@@ -1024,6 +1077,7 @@ private:
     // caller (graph_segment puts them between its graphs)
     void EnqueueTask(RankCtx &rc, Launch &L, hipStream_t s, bool events = true)
     {
+        if (L.skip) return;  // computed in its producer GEMM's epilogue
         const NodeSpec &n = *L.node;
         const TaskSpec &t = *L.task;
         NodeBuf &b = rc.bufs.at(n.id);
@@ -1059,6 +1113,14 @@ private:
             d.N = int(ncols);
             d.K = int(n.k);
             d.coresident = L.coresident;
+            if (L.epi != nullptr) {
+                // the in-register relay: the consumer's rows leave with C's
+                const NodeSpec &c = *L.epi;
+                d.y = static_cast<char *>(rc.bufs.at(c.id).out.get()) + size_t(out_off) * c.cols * DTypeBytes(c.out_dtype);
+                d.y_op = c.op == Op::Gelu ? kEwGelu : (c.op == Op::Silu ? kEwSilu : kEwCast);
+                d.y_dtype = c.out_dtype;
+                d.ld_y = c.cols;
+            }
             if (pub.ctrl && GemmPickTile(d.M, d.N, pub.rows_per_tile, d.coresident).bm < 0) {
                 // the tile cannot be one GEMM relay tile: release after the GEMM
                 GemmLaunch(d, s);
@@ -1207,7 +1269,7 @@ private:
             for (int lane = 0; lane < 2; ++lane) {
                 bool any = false;
                 for (size_t idx : enqueue_order_)
-                    if (launches_[idx].lane == lane) any = true;
+                    if (launches_[idx].lane == lane && !launches_[idx].skip) any = true;
                 if (!any) continue;
                 hipStream_t s = StreamOf(lane);
                 hipGraph_t g = nullptr;
@@ -1416,6 +1478,7 @@ int RunPlan(const char *schedule_json, int iters, int warmup, const char *device
         result.Set("sync", Value::MakeString(ex.sync()));
         result.Set("mode", Value::MakeString(mode ? mode : "direct"));
         result.Set("flag_edges", Value::MakeNumber(ex.edges()));
+        result.Set("epilogue_consumers", Value::MakeNumber(ex.epilogue_consumers()));
         result.Set("consumer_cus", Value::MakeNumber(ex.consumer_cus()));
         json::WriteFile(out_json, result);
         std::printf("%s\n", result.Dump().c_str());

@@ -40,19 +40,6 @@ struct EwParams {
     RelayPub pub;
 };
 
-// GELU, tanh form: 0.5 x (1 + tanh(y)), y = sqrt(2/pi) (x + 0.044715 x^3),
-// computed as the identical x / (1 + e^(-2y)) (1 + tanh(y) = 2 / (1 + e^(-2y))):
-// five full-rate operations and two transcendentals per element. Saturates
-// through the exponential: e^(-2y) -> inf gives -0 for large negative x,
-// -> 0 gives x for large positive x.
-__device__ __forceinline__ float GeluTanh(float x)
-{
-    const float c = -2.0f * 0.7978845608028654f * 1.4426950408889634f;  // -2 sqrt(2/pi) log2(e)
-    const float u = 1.0f + 0.044715f * (x * x);
-    return x * FastRcp(1.0f + __builtin_amdgcn_exp2f(c * x * u));
-}
-
-
 template <int OP, int DTI, int DTO>
 __global__ void __launch_bounds__(kThreads) EwKernel(EwParams p)
 {
@@ -64,41 +51,52 @@ __global__ void __launch_bounds__(kThreads) EwKernel(EwParams p)
         RelayWaitRows(p.w, r_lo, r_hi);
         const int64_t c0 = int64_t(t) * p.tile_chunks;
         const int64_t c1 = min(c0 + p.tile_chunks, p.total_chunks);
-        for (int64_t c = c0 + int64_t(blockIdx.x) * kThreads + threadIdx.x; c < c1; c += stride) {
-            U16x8 a, b;
-            if constexpr (OP == kEwSwigluGU) {
-                // fused gate/up rows: 8 gate columns then the matching 8 up columns
-                a = LoadU16x8(p.x0 + c * 16);
-                b = LoadU16x8(p.x0 + c * 16 + 8);
-            } else {
-                a = LoadU16x8(p.x0 + c * 8);
-                if constexpr (OP == kEwMul || OP == kEwAdd || OP == kEwSwiglu) b = LoadU16x8(p.x1 + c * 8);
-            }
-            float o[8];
+        if constexpr (DTO == kF32) {
+            // 4 values per step (8-byte loads, 16-byte stores): every store
+            // instruction of the wave covers whole 128-byte lines of y
+            static_assert(OP == kEwCast || OP == kEwGelu || OP == kEwSilu, "fp32 output of a unary op");
+            for (int64_t h = 2 * c0 + int64_t(blockIdx.x) * kThreads + threadIdx.x; h < 2 * c1; h += stride) {
+                const uint2 u = *reinterpret_cast<const uint2 *>(p.x0 + h * 4);
+                const uint16_t a[4] = {uint16_t(u.x), uint16_t(u.x >> 16), uint16_t(u.y), uint16_t(u.y >> 16)};
+                float o[4];
 #pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                const float x = Elem<DTI>::Load(a.v[e]);
-                if constexpr (OP == kEwGelu) {
-                    o[e] = GeluTanh(x);
-                } else if constexpr (OP == kEwSilu) {
-                    o[e] = Silu(x);
-                } else if constexpr (OP == kEwCast) {
-                    o[e] = x;
-                } else if constexpr (OP == kEwMul) {
-                    o[e] = x * Elem<DTI>::Load(b.v[e]);
-                } else if constexpr (OP == kEwAdd) {
-                    o[e] = x + Elem<DTI>::Load(b.v[e]);
-                } else {  // swiglu: the silu result is stored (rounded) before the multiply
-                    o[e] = RoundTo<DTI>(Silu(x)) * Elem<DTI>::Load(b.v[e]);
+                for (int e = 0; e < 4; ++e) {
+                    const float x = Elem<DTI>::Load(a[e]);
+                    o[e] = OP == kEwGelu ? GeluTanh(x) : (OP == kEwSilu ? Silu(x) : x);
                 }
+                PutU128(static_cast<float *>(p.y) + h * 4,
+                        make_uint4(__float_as_uint(o[0]), __float_as_uint(o[1]), __float_as_uint(o[2]),
+                                   __float_as_uint(o[3])), coh);
             }
-            if constexpr (DTO == kF32) {
-                float *yp = static_cast<float *>(p.y) + c * 8;
-                PutU128(yp, make_uint4(__float_as_uint(o[0]), __float_as_uint(o[1]), __float_as_uint(o[2]),
-                                       __float_as_uint(o[3])), coh);
-                PutU128(yp + 4, make_uint4(__float_as_uint(o[4]), __float_as_uint(o[5]), __float_as_uint(o[6]),
-                                           __float_as_uint(o[7])), coh);
-            } else {
+        } else {
+            for (int64_t c = c0 + int64_t(blockIdx.x) * kThreads + threadIdx.x; c < c1; c += stride) {
+                U16x8 a, b;
+                if constexpr (OP == kEwSwigluGU) {
+                    // fused gate/up rows: 8 gate columns then the matching 8 up columns
+                    a = LoadU16x8(p.x0 + c * 16);
+                    b = LoadU16x8(p.x0 + c * 16 + 8);
+                } else {
+                    a = LoadU16x8(p.x0 + c * 8);
+                    if constexpr (OP == kEwMul || OP == kEwAdd || OP == kEwSwiglu) b = LoadU16x8(p.x1 + c * 8);
+                }
+                float o[8];
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    const float x = Elem<DTI>::Load(a.v[e]);
+                    if constexpr (OP == kEwGelu) {
+                        o[e] = GeluTanh(x);
+                    } else if constexpr (OP == kEwSilu) {
+                        o[e] = Silu(x);
+                    } else if constexpr (OP == kEwCast) {
+                        o[e] = x;
+                    } else if constexpr (OP == kEwMul) {
+                        o[e] = x * Elem<DTI>::Load(b.v[e]);
+                    } else if constexpr (OP == kEwAdd) {
+                        o[e] = x + Elem<DTI>::Load(b.v[e]);
+                    } else {  // swiglu: the silu result is stored (rounded) before the multiply
+                        o[e] = RoundTo<DTI>(Silu(x)) * Elem<DTI>::Load(b.v[e]);
+                    }
+                }
                 U16x8 r;
 #pragma unroll
                 for (int e = 0; e < 8; ++e) r.v[e] = Elem<DTO>::Store(o[e]);

@@ -7,7 +7,10 @@
   relay split at k = 1, 2, 4, 8 (schedules from kernrelay_amd.schedule, as
   the reference's E3/E4 variants, python/kernrelay/e34.py:16-22);
 * the reference's own relay cases (fp16 32768x1024x2048 GEMM -> GELU,
-  softmax, cast, {GELU, softmax}) at its k, next to its published times.
+  softmax, cast, {GELU, softmax}) at its k, next to its published times;
+  for an elementwise consumer also the in-register relay (the same split
+  schedule with the consumer computed in the GEMM's epilogue,
+  KR_PLAN_EPILOGUE=1).
 
 Each variant runs as a replayed graph per stream (`graph_per_stream`); the
 reported time is the device makespan (HIP events on both streams, best and
@@ -54,11 +57,20 @@ def _stdout_to_stderr():
         os.close(saved)
 
 
-def _plan(sched, tmp, name, iters, warmup, mode="graph_per_stream"):
+def _plan(sched, tmp, name, iters, warmup, mode="graph_per_stream", env=None):
     path = schedule.dump_schedule(sched, Path(tmp) / (name + ".json"))
-    with _stdout_to_stderr():
-        r = libapi.plan_run(path, devices="0", mode=mode, iters=iters, warmup=warmup,
-                            out_json=Path(tmp) / (name + "_out.json"))
+    saved = {k: os.environ.get(k) for k in (env or {})}
+    os.environ.update(env or {})
+    try:
+        with _stdout_to_stderr():
+            r = libapi.plan_run(path, devices="0", mode=mode, iters=iters, warmup=warmup,
+                                out_json=Path(tmp) / (name + "_out.json"))
+    finally:
+        for k, v in saved.items():
+            if v is None:
+                os.environ.pop(k, None)
+            else:
+                os.environ[k] = v
     if r.get("_rc") != 0 or not r.get("ok"):
         raise RuntimeError("kr_plan_run %s failed: %s" % (name, r))
     return r
@@ -120,15 +132,22 @@ def reference_e34(tmp, iters=20, warmup=3):
         dag = workloads.e34_dag(case, consumers)
         v = workloads.variants(dag, k)
         rs = {name: _plan(v[name], tmp, "%s_%s" % (case, name), iters, warmup) for name in ("serial", "b0", "split")}
+        if len(consumers) == 1 and consumers[0] in ("gelu", "silu", "cast"):
+            # the same split schedule with the consumer in the GEMM's epilogue
+            rs["register_relay"] = _plan(v["split"], tmp, "%s_epi" % case, iters, warmup, env={"KR_PLAN_EPILOGUE": "1"})
         ours = {name: round(rs[name]["device_best_us"], 2) for name in rs}
         out[case] = {
             "k": k,
             "serial_us": ours["serial"], "b0_us": ours["b0"], "split_us": ours["split"],
             "serial_over_split": round(ours["serial"] / ours["split"], 4),
+            "flag_edges": rs["split"]["flag_edges"],
             "reference_serial_over_split": round(r_serial / r_split, 4),
             "reference_us": {"serial": r_serial, "b0": r_b0, "split": r_split},
             "checksums_equal": len({rs[n]["checksum"] for n in rs}) == 1,
         }
+        if "register_relay" in rs:
+            out[case]["register_relay_us"] = ours["register_relay"]
+            out[case]["serial_over_register_relay"] = round(ours["serial"] / ours["register_relay"], 4)
     return out
 
 

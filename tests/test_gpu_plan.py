@@ -115,6 +115,39 @@ def test_graph_segment_reference_checksums(gpu, tmp_path, name, consumers, expec
     assert abs(r["checksum"] - expected) / abs(expected) < 1e-3, (r["checksum"], expected)
 
 
+@pytest.mark.parametrize("name,consumers,k", [("f01_mm_gelu_c2", ["gelu"], 4), ("e3_mm_cast", ["cast"], 2),
+                                              ("e3_mm_silu", ["silu"], 8)])
+def test_epilogue_relay_bit_exact(gpu, tmp_path, name, consumers, k):
+    """The in-register relay (KR_PLAN_EPILOGUE=1): the reference's e34 DAG
+    split at k with its GELU / cast (fp16 -> fp32) / SiLU consumer computed
+    in the GEMM's epilogue equals the serial schedule bit for bit (both
+    outputs), runs no consumer launch and no relay edge, and reproduces the
+    reference's checksum where it has one."""
+    dag = workloads.e34_dag(name, consumers)
+    _, base = run(schedule.serial_schedule(dag), tmp_path, "serial", iters=1, warmup=0)
+    sched = workloads.variants(dag, k)["split"]
+    r, outs = run(sched, tmp_path, "epi", mode="graph_per_stream", env={"KR_PLAN_EPILOGUE": "1"})
+    assert r["ok"] and r["epilogue_consumers"] == 1 and r["flag_edges"] == 0, r
+    for node in base:
+        assert np.array_equal(base[node], outs[node]), node
+    expected = {kk[0]: kk[2] for kk in KATS}.get(name)
+    if expected is not None:
+        r2 = libapi.plan_run(schedule.dump_schedule(schedule.build_fixed_schedule(dag, {n.name: 4 for n in dag.nodes},
+                                                                                  nranks=2), tmp_path / "kat.json"),
+                             devices="0,0", mode="direct", iters=1, warmup=0, out_json=tmp_path / "kat_out.json")
+        assert r2["_rc"] == 0 and r2["ok"]
+        # (KR_PLAN_EPILOGUE is unset here: the plain relay's checksum)
+        assert abs(r2["checksum"] - expected) / abs(expected) < 1e-3
+        os.environ["KR_PLAN_EPILOGUE"] = "1"
+        try:
+            r3 = libapi.plan_run(tmp_path / "kat.json", devices="0,0", mode="direct", iters=1, warmup=0,
+                                 out_json=tmp_path / "kat_out3.json")
+        finally:
+            del os.environ["KR_PLAN_EPILOGUE"]
+        assert r3["_rc"] == 0 and r3["ok"] and r3["epilogue_consumers"] >= 1
+        assert abs(r3["checksum"] - expected) / abs(expected) < 1e-3, (r3["checksum"], expected)
+
+
 def test_wait_kernel_variant_matches(gpu, tmp_path):
     dag = workloads.tiny_mm_gelu(tmp_path)
     sched = schedule.build_fixed_schedule(dag, {"mm": 2, "gelu": 2})
