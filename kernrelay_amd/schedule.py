@@ -1,20 +1,24 @@
 """DAG model and fixed row-split schedules consumed by kr_plan_run.
 
-Behaviour follows the reference's scheduler for this path:
+The schedule.json format, the tile geometry and the rejection markers are
+the reference's interface for this path; the code is this module's own:
 
-* ``build_fixed_schedule`` — the schedule.json the reference's fixed-plan
-  writer emits (python/kernrelay/_vendor/scheduler/fixed.py:64-156): every
-  node's input rows are split evenly into its chunk count; consumer tile j
-  waits on every producer tile whose output rows meet j's input rows (the
-  last producer tile when none do); waits exist only across streams; tasks
-  enter their stream in DAG topological order (declaration order breaks
-  ties);
+* ``build_fixed_schedule`` — the schedule the reference's fixed-plan writer
+  emits (python/kernrelay/_vendor/scheduler/fixed.py:64-156), built as a
+  relation: every node's input rows cut evenly into its chunk count; a
+  consumer tile waits on the producer tiles whose output rows meet its
+  input rows (the last producer tile when none do), across streams only; a
+  task publishes exactly when something waits on it; each stream's FIFO is
+  its tasks sorted by (topological rank of the node, tile), declaration
+  order breaking ties between nodes;
 * ``serial_schedule`` — the reference's serial baseline
-  (python/kernrelay/schedule.py:67-105): all tiles on one ``aicore`` stream
-  in a global topological order, no waits or publishes;
-* ``validate_schedule`` / ``invalid_variants`` — structural checks, and the
-  four deliberately broken schedules whose executor error markers the
-  reference's E0 gate expects (python/kernrelay/schedule.py:108-222).
+  (python/kernrelay/schedule.py:67-105) as a list schedule over the unsplit
+  schedule's happens-before graph, ties going to the stream of higher
+  precedence, then to the earlier FIFO position;
+* ``validate_schedule`` / ``invalid_variants`` — structural checks that name
+  the offending task or cycle, and broken schedules for the four executor
+  error markers the reference's E0 gate expects
+  (python/kernrelay/schedule.py:108-222).
 
 Op -> stream follows the reference's measured engine map
 (python/kernrelay/_vendor/registry/engine_map.json): matrix work on ``aic``,
@@ -222,207 +226,274 @@ def row_splits(dag, chunking, nranks):
     return out
 
 
-def _task(node, tile, split):
-    return {"node": node, "tile": tile, "wait": [], "publish": False, "in_row_off": tile * split.in_rows,
-            "in_rows": split.in_rows, "out_row_off": tile * split.out_rows}
+TaskKey = tuple  # (node name, tile index)
+
+
+def _key(task):
+    """(node, tile) of a schedule.json task record."""
+    return task.get("node"), int(task.get("tile", 0))
+
+
+def _cross_stream_waits(dag, splits):
+    """The wait relation of a row-tiled DAG: {consumer task: [producer
+    tasks]}. Only edges whose two ends run on different streams wait (a
+    stream's FIFO already orders the rest). A consumer tile waits on the
+    producer tiles whose output rows meet its input rows, taken edge by
+    edge in the DAG's edge order, tiles ascending."""
+    by_name = dag.node_map
+    relation = {}
+    for e in dag.edges:
+        if stream_of(by_name[e.src].op) == stream_of(by_name[e.dst].op):
+            continue
+        made, used = splits[e.src], splits[e.dst]
+        for j in range(used.chunks):
+            lo = j * used.in_rows
+            relation.setdefault((e.dst, j), []).extend(
+                (e.src, k) for k in made.tiles_covering(lo, lo + used.in_rows))
+    return relation
+
+
+def _node_entry(node, chunks, preds):
+    """schedule.json "nodes" record: the executor's fields for one node."""
+    entry = dict(id=node.name, op=node.op, engine=stream_of(node.op), dtype=node.dtype, tiles=chunks,
+                 split=chunks > 1, preds=preds, iters=1, blocks=1)
+    entry.update(node_dims(node))
+    entry.update(node.extra)
+    return entry
 
 
 def build_fixed_schedule(dag, chunking=None, nranks=1, method="fixed"):
-    """DAG + per-node chunk counts -> schedule.json content (dict), the
-    format of the reference's fixed-plan writer
+    """DAG + per-node chunk counts -> schedule.json content (dict), in the
+    format the reference's fixed-plan writer emits
     (python/kernrelay/_vendor/scheduler/fixed.py:64-156).
 
-    Each node's rows are cut into equal tiles. A consumer tile waits on every
-    producer tile whose output rows meet its input rows, but only across
-    streams (one stream's FIFO already orders its tasks), and those producer
-    tiles publish. Tasks join their op's stream in dependency order."""
+    Built as a relation rather than task by task: every (node, tile) task
+    gets its equal share of the node's rows; the wait relation comes from
+    the row cuts (`_cross_stream_waits`); a task publishes exactly when some
+    task waits on it; and each stream's FIFO is the set of its tasks sorted
+    by (topological rank of the node, tile)."""
     chunking = {k: int(v) for k, v in dict(chunking or {}).items() if int(v) > 0}
     by_name = dag.node_map
     unknown = sorted(set(chunking) - set(by_name))
     if unknown:
         raise ValueError("%s: chunking names unknown nodes %s" % (dag.name, unknown))
-    sinks_only = [e for e in dag.edges if by_name[e.src].op == "cast"]
-    if sinks_only:
-        raise ValueError("%s: a cast output may only be a sink, not consumed by %s" % (dag.name, sinks_only[0].dst))
-    splits = row_splits(dag, chunking, nranks)
-    tasks = {(n.name, t): _task(n.name, t, splits[n.name]) for n in dag.nodes for t in range(splits[n.name].chunks)}
-
     for e in dag.edges:
         src, dst = by_name[e.src], by_name[e.dst]
+        if src.op == "cast":
+            raise ValueError("%s: a cast output may only be a sink, not consumed by %s" % (dag.name, e.dst))
         if node_rows(dst) > out_rows(src, nranks):
             raise ValueError("%s: edge %s->%s consumer reads %d rows but the producer writes %d"
                              % (dag.name, e.src, e.dst, node_rows(dst), out_rows(src, nranks)))
-        if stream_of(src.op) == stream_of(dst.op):
-            continue
-        ps, cs = splits[src.name], splits[dst.name]
-        for j in range(cs.chunks):
-            for k in ps.tiles_covering(j * cs.in_rows, (j + 1) * cs.in_rows):
-                tasks[(dst.name, j)]["wait"].append([src.name, k])
-                tasks[(src.name, k)]["publish"] = True
-
+    splits = row_splits(dag, chunking, nranks)
+    waits = _cross_stream_waits(dag, splits)
+    waited_on = {w for ws in waits.values() for w in ws}
+    rank = {name: r for r, name in enumerate(topo_order(dag))}
+    keys = sorted(((n.name, t) for n in dag.nodes for t in range(splits[n.name].chunks)),
+                  key=lambda k: (rank[k[0]], k[1]))
     streams = {}
-    for name in topo_order(dag):
-        lane = streams.setdefault(stream_of(by_name[name].op), [])
-        lane.extend(tasks[(name, t)] for t in range(splits[name].chunks))
-
-    nodes = []
-    for n in dag.nodes:
-        k = splits[n.name].chunks
-        entry = {"id": n.name, "op": n.op, "engine": stream_of(n.op), "dtype": n.dtype, "tiles": k,
-                 "split": k > 1, "preds": [e.src for e in dag.edges if e.dst == n.name], "iters": 1, "blocks": 1}
-        entry.update(node_dims(n))
-        entry.update(n.extra)
-        nodes.append(entry)
-    return {"dag": dag.name, "group": method, "nranks": int(nranks), "nodes": nodes,
-            "streams": {k: v for k, v in streams.items() if v},
-            "chunking": {k: v for k, v in chunking.items() if v > 1}, "fallback": ""}
+    for name, tile in keys:
+        cut = splits[name]
+        streams.setdefault(stream_of(by_name[name].op), []).append({
+            "node": name, "tile": tile, "wait": [list(w) for w in waits.get((name, tile), [])],
+            "publish": (name, tile) in waited_on, "in_row_off": tile * cut.in_rows, "in_rows": cut.in_rows,
+            "out_row_off": tile * cut.out_rows})
+    preds = {n.name: [] for n in dag.nodes}
+    for e in dag.edges:
+        preds[e.dst].append(e.src)
+    return {"dag": dag.name, "group": method, "nranks": int(nranks),
+            "nodes": [_node_entry(n, splits[n.name].chunks, preds[n.name]) for n in dag.nodes],
+            "streams": streams, "chunking": {k: v for k, v in chunking.items() if v > 1}, "fallback": ""}
 
 
-# Which stream's head goes first when several could run next in the serial
-# baseline (the reference's precedence, python/kernrelay/schedule.py:67-105):
-# mixed work, then matrix, vector, CPU and collective streams; "compute" is
-# another name of "aicore".
-STREAM_PRECEDENCE = ("aicore", "aic", "aiv", "aicpu", "hccl")
-
-
-def _precedence(stream):
+def _stream_precedence(stream):
+    """Serial tie-break between streams: the order of ENGINES (mixed work,
+    matrix, vector, CPU, collectives); "compute" is the mixed stream's other
+    name, unknown names go last."""
     stream = "aicore" if stream == "compute" else stream
-    return STREAM_PRECEDENCE.index(stream) if stream in STREAM_PRECEDENCE else len(STREAM_PRECEDENCE)
+    return ENGINES.index(stream) if stream in ENGINES else len(ENGINES)
+
+
+def _happens_before(streams):
+    """{task: set of tasks that must finish first} of a schedule's streams:
+    each task's FIFO predecessor and the tasks it waits on."""
+    before = {}
+    for seq in streams.values():
+        prev = None
+        for t in seq:
+            deps = before.setdefault(_key(t), set())
+            deps.update((w[0], int(w[1])) for w in t.get("wait") or [])
+            if prev is not None:
+                deps.add(prev)
+            prev = _key(t)
+    return before
 
 
 def serial_schedule(dag, nranks=1):
-    """Serial baseline: every tile of the unsplit schedule on one ``aicore``
-    stream, no waits or publishes. The per-stream FIFOs of the unsplit
-    schedule are merged: a stream's head may go once every task it waits on
-    has gone, and of the heads that may go, the stream of highest precedence
-    goes first."""
+    """Serial baseline (the reference's, python/kernrelay/schedule.py:67-105):
+    every task of the unsplit schedule on one ``aicore`` stream, no waits or
+    publishes. The order is a list schedule of the unsplit schedule's
+    happens-before graph: of the tasks whose predecessors have all gone, the
+    one with the smallest (stream precedence, FIFO position) goes next."""
+    import heapq
     base = build_fixed_schedule(dag, {}, nranks=nranks, method="serial")
-    lanes = sorted(base["streams"].items(), key=lambda kv: _precedence(kv[0]))
-    heads = [0] * len(lanes)
-    placed, merged = set(), []
-    total = sum(len(seq) for _, seq in lanes)
-    while len(merged) < total:
-        for i, (_, seq) in enumerate(lanes):
-            if heads[i] < len(seq) and all((w[0], int(w[1])) in placed for w in seq[heads[i]].get("wait") or []):
-                t = seq[heads[i]]
-                heads[i] += 1
-                placed.add((t["node"], int(t.get("tile", 0))))
-                merged.append(dict(t, wait=[], publish=False))
-                break
-        else:
-            raise RuntimeError("%s: the serial baseline cannot order its streams (wait cycle)" % dag.name)
+    record, priority = {}, {}
+    for stream, seq in base["streams"].items():
+        for pos, t in enumerate(seq):
+            record[_key(t)] = t
+            priority[_key(t)] = (_stream_precedence(stream), pos)
+    before = _happens_before(base["streams"])
+    pending = {k: len(v) for k, v in before.items()}
+    after = {k: [] for k in before}
+    for k, deps in before.items():
+        for d in deps:
+            after[d].append(k)
+    ready = [(priority[k], k) for k, n in pending.items() if n == 0]
+    heapq.heapify(ready)
+    order = []
+    while ready:
+        _, k = heapq.heappop(ready)
+        order.append(dict(record[k], wait=[], publish=False))
+        for nxt in after[k]:
+            pending[nxt] -= 1
+            if pending[nxt] == 0:
+                heapq.heappush(ready, (priority[nxt], nxt))
+    if len(order) != len(record):
+        raise RuntimeError("%s: the serial baseline cannot order its streams (wait cycle)" % dag.name)
     out = dict(base)
-    out.update(streams={"aicore": merged}, group="serial", chunking={})
+    out.update(streams={"aicore": order}, group="serial", chunking={})
     return out
+
+
+def _find_cycle(before):
+    """One cycle of a {task: predecessors} graph as a task list (first ==
+    last), or None. Depth-first, iterative, with the path kept on a stack."""
+    colour = {}
+    for root in before:
+        if root in colour:
+            continue
+        path, iters = [root], [iter(sorted(before[root], key=repr))]
+        colour[root] = "open"
+        while path:
+            nxt = next(iters[-1], None)
+            if nxt is None:
+                colour[path.pop()] = "done"
+                iters.pop()
+            elif colour.get(nxt) == "open":
+                return path[path.index(nxt):] + [nxt]
+            elif nxt not in colour:
+                colour[nxt] = "open"
+                path.append(nxt)
+                iters.append(iter(sorted(before.get(nxt, ()), key=repr)))
+    return None
 
 
 def validate_schedule(sched):
-    """Structural checks of a schedule.json dict (the executor stays the
-    authority): node ids, stream names, tasks, waits on publishing tasks and
-    a happens-before order without cycles (stream FIFO + waits). Returns the
-    list of problems found."""
-    errors = []
-    ids = [n.get("id") for n in sched.get("nodes") or []]
-    if len(ids) != len(set(ids)):
-        errors.append("duplicate node ids")
+    """Problems found in a schedule.json dict, as messages (empty: none);
+    the executor stays the authority. Checked: node ids unique; streams
+    named for engines and holding task lists; every task of a declared
+    node, on one stream only, with in_rows > 0; every wait on an existing
+    task that publishes; and the happens-before graph (FIFO + waits) free of
+    cycles, one of which is named when present."""
+    problems = []
+    declared = [n.get("id") for n in sched.get("nodes") or []]
+    if len(declared) != len(set(declared)):
+        problems.append("node ids are not unique")
     streams = sched.get("streams") or {}
     if not streams:
-        errors.append("no streams")
-    where, publishing = {}, set()
-    before = {}  # task -> tasks that must finish first
-    for engine, seq in streams.items():
-        if engine not in ENGINES:
-            errors.append("unknown stream %r" % engine)
-        if not isinstance(seq, list):
-            errors.append("stream %r is not a task list" % engine)
-            continue
-        prev = None
+        problems.append("the schedule has no streams")
+    lists = {}
+    for name, seq in streams.items():
+        if name not in ENGINES:
+            problems.append("stream %r is not an engine" % name)
+        if isinstance(seq, list):
+            lists[name] = seq
+        else:
+            problems.append("stream %r is not a task list" % name)
+    home = {}
+    for name, seq in lists.items():
         for t in seq:
-            key = (t.get("node"), int(t.get("tile", 0)))
-            if key[0] not in ids:
-                errors.append("stream %s task names unknown node %r" % (engine, key[0]))
-            if key in where:
-                errors.append("node %s tile %d repeated on streams %s/%s" % (key[0], key[1], where[key], engine))
-            where[key] = engine
+            k = _key(t)
+            if k[0] not in declared:
+                problems.append("a task on stream %s belongs to unknown node %r" % (name, k[0]))
+            if k in home:
+                problems.append("task %s#%d repeated on streams %s and %s" % (k[0], k[1], home[k], name))
+            home.setdefault(k, name)
             if int(t.get("in_rows", 1)) <= 0:
-                errors.append("node %s tile %d has in_rows <= 0" % key)
-            if t.get("publish"):
-                publishing.add(key)
-            before.setdefault(key, set())
-            if prev is not None:
-                before[key].add(prev)
-            prev = key
-    for seq in streams.values():
-        for t in seq if isinstance(seq, list) else []:
-            key = (t.get("node"), int(t.get("tile", 0)))
+                problems.append("task %s#%d reads no rows" % k)
+    publishes = {_key(t) for seq in lists.values() for t in seq if t.get("publish")}
+    for seq in lists.values():
+        for t in seq:
             for w in t.get("wait") or []:
                 dep = (w[0], int(w[1]))
-                if dep not in where:
-                    errors.append("node %s tile %d waits on missing task %s#%s" % (key[0], key[1], dep[0], dep[1]))
-                    continue
-                if dep not in publishing:
-                    errors.append("node %s tile %d waits on %s#%s which never publishes"
-                                  % (key[0], key[1], dep[0], dep[1]))
-                before[key].add(dep)
-    # a cycle in the happens-before relation: iterative three-colour DFS
-    state = {}
-    for root in before:
-        if state.get(root):
-            continue
-        stack = [(root, iter(before[root]))]
-        state[root] = 1
-        while stack:
-            node, deps = stack[-1]
-            nxt = next(deps, None)
-            if nxt is None:
-                state[node] = 2
-                stack.pop()
-            elif state.get(nxt) == 1:
-                errors.append("schedule has a wait cycle")
-                return errors
-            elif not state.get(nxt):
-                state[nxt] = 1
-                stack.append((nxt, iter(before.get(nxt, ()))))
-    return errors
+                if dep not in home:
+                    problems.append("task %s#%d waits on %s#%d, which no stream runs" % (_key(t) + dep))
+                elif dep not in publishes:
+                    problems.append("task %s#%d waits on %s#%d, which never publishes" % (_key(t) + dep))
+    cycle = _find_cycle({k: {d for d in v if d in home} for k, v in _happens_before(lists).items()})
+    if cycle:
+        problems.append("wait cycle: " + " -> ".join("%s#%d" % k for k in cycle))
+    return problems
+
+
+def _task_streams(sched):
+    return [name for name, seq in sched["streams"].items() if seq]
+
+
+def _alias_mixed_stream(sched):
+    """The mixed stream under both of its names (an empty ``aicore`` and an
+    empty ``compute`` lane beside the others)."""
+    sched["streams"].setdefault("aicore", [])
+    sched["streams"]["compute"] = []
+    return sched
+
+
+def _undeclared_node(sched):
+    """A copy of the last task of the first stream, for a node the schedule
+    does not declare."""
+    seq = sched["streams"][_task_streams(sched)[0]]
+    seq.append(dict(seq[-1], node="undeclared_node", wait=[], publish=False))
+    return sched
+
+
+def _crossed_waits(sched):
+    """The first task of the second stream waits on the last task of the
+    first stream, which waits on it in turn."""
+    first, second = (sched["streams"][s] for s in _task_streams(sched)[:2])
+    tail, head = first[-1], second[0]
+    for x, y in ((tail, head), (head, tail)):
+        x["publish"] = True
+        x["wait"] = list(x.get("wait") or []) + [list(_key(y))]
+    return sched
+
+
+def _shifted_past_rows(sched):
+    """The last task of the first stream reads starting past every row that
+    any node of the schedule produces."""
+    past = sum(int(n["rows"]) for n in sched["nodes"]) * max(1, int(sched.get("nranks", 1))) + 1
+    sched["streams"][_task_streams(sched)[0]][-1]["in_row_off"] = past
+    return sched
+
+
+# The reference's four executor rejection cases
+# (python/kernrelay/schedule.py:185-222): label -> (mutation, the marker the
+# executor's error must contain, streams with tasks the mutation needs).
+# The markers are the executor's interface; the mutations are this module's.
+REJECTION_CASES = {
+    "duplicate_engine": (_alias_mixed_stream, "duplicate engine stream", 1),
+    "ghost_task": (_undeclared_node, "missing plan for task", 1),
+    "wait_cycle": (_crossed_waits, "wait cycle", 2),
+    "row_overflow": (_shifted_past_rows, "exceed", 1),
+}
 
 
 def invalid_variants(sched):
-    """Broken copies of a valid schedule, each paired with the error marker
-    the executor must reject it with (the four cases of the reference's E0
-    rejection gate, python/kernrelay/schedule.py:185-222, whose markers are
-    the executor's interface):
-      duplicate_engine  a second name for the mixed stream holds tasks too
-      ghost_task        a task of a node the schedule does not declare
-      wait_cycle        the first tasks of two streams wait on each other
-      row_overflow      a tile reads far past its node's rows"""
-    out = {}
-    named = [k for k, v in sched["streams"].items() if v]
-
-    dup = copy.deepcopy(sched)
-    moved = dup["streams"].pop(named[0])
-    dup["streams"]["aicore"] = []
-    dup["streams"]["compute"] = moved
-    out["duplicate_engine"] = (dup, "duplicate engine stream")
-
-    ghost = copy.deepcopy(sched)
-    ghost["streams"][named[0]].append(
-        {"node": "__ghost__", "tile": 0, "wait": [], "publish": False, "in_row_off": 0, "in_rows": 1})
-    out["ghost_task"] = (ghost, "missing plan for task")
-
-    if len(named) >= 2:
-        cyc = copy.deepcopy(sched)
-        a, b = cyc["streams"][named[0]][0], cyc["streams"][named[1]][0]
-        for x, y in ((a, b), (b, a)):
-            x["publish"] = True
-            x.setdefault("wait", []).append([y["node"], int(y.get("tile", 0))])
-        out["wait_cycle"] = (cyc, "wait cycle")
-
-        over = copy.deepcopy(sched)
-        later = [t for seq in over["streams"].values() for t in seq if t.get("in_row_off", 0) > 0]
-        if later:
-            later[0]["in_rows"] = int(later[0]["in_rows"]) + 10 ** 9
-            out["row_overflow"] = (over, "exceed")
-    return out
+    """Broken copies of a valid schedule: {label: (schedule, marker)}, the
+    executor must reject each with an error containing its marker. A case
+    that needs more task-holding streams than the schedule has is left
+    out."""
+    have = len(_task_streams(sched))
+    return {label: (mutate(copy.deepcopy(sched)), marker)
+            for label, (mutate, marker, needs) in REJECTION_CASES.items() if have >= needs}
 
 
 def dump_schedule(sched, path):

@@ -120,3 +120,64 @@ def test_validator_flags_broken_schedules(tmp_path):
 def test_rows_must_divide():
     with pytest.raises(ValueError, match="not divisible"):
         schedule.build_fixed_schedule(mm_chain(1000), {"mm": 3})
+
+
+def test_validator_names_the_cycle_and_every_case_trips_it(tmp_path):
+    """The cycle message lists the tasks on it; each broken variant is flagged
+    by the validator too (the executor's markers are checked in test_abi)."""
+    dag = workloads.tiny_mm_gelu(tmp_path)
+    sched = schedule.build_fixed_schedule(dag, {"mm": 2, "gelu": 2})
+    bad = schedule.invalid_variants(sched)
+    msg = [e for e in schedule.validate_schedule(bad["wait_cycle"][0]) if "wait cycle" in e]
+    assert len(msg) == 1
+    path = msg[0].split(": ", 1)[1].split(" -> ")
+    assert path[0] == path[-1] and len(path) >= 3
+    assert set(path) >= {"mm#1", "gelu#0"}
+    assert any("not an engine" in e for e in schedule.validate_schedule(bad["duplicate_engine"][0]))
+    assert schedule.validate_schedule(bad["row_overflow"][0]) == []  # rows are the executor's check
+
+
+def test_single_stream_schedule_variants():
+    """A schedule with one task-holding stream (the serial baseline) still
+    yields the cases that need one stream; the wait cycle needs two."""
+    sched = schedule.serial_schedule(mm_chain(512))
+    bad = schedule.invalid_variants(sched)
+    assert set(bad) == {"duplicate_engine", "ghost_task", "row_overflow"}
+    over = bad["row_overflow"][0]["streams"]["aicore"][-1]
+    assert over["in_row_off"] > max(n["rows"] for n in sched["nodes"])
+
+
+def test_serial_schedule_is_a_priority_list_schedule():
+    """On random DAGs the serial order respects every happens-before edge of
+    the unsplit schedule, and whenever a task goes, no ready task of a
+    stream with higher precedence (or earlier in the same FIFO) was left."""
+    import random
+    rng = random.Random(3)
+    ops = ["matmul", "gelu", "softmax", "cast", "add", "topk", "allreduce"]
+    for trial in range(150):
+        n = rng.randint(1, 6)
+        nodes = []
+        for i in range(n):
+            op = rng.choice(ops)
+            shape = {"M": 128, "K": 64, "N": 64} if op == "matmul" else (
+                {"rows": 128, "cols": 64, "k": 2} if op == "topk" else {"rows": 128, "cols": 64})
+            nodes.append({"name": "n%d" % i, "op": op, "shape": shape})
+        edges = [{"src": "n%d" % i, "dst": "n%d" % j} for i in range(n) for j in range(i + 1, n)
+                 if rng.random() < 0.4 and nodes[i]["op"] != "cast"]
+        dag = schedule.dag_from_dict({"name": "t%d" % trial, "nodes": nodes, "edges": edges})
+        base = schedule.build_fixed_schedule(dag, {})
+        prio = {}
+        before = {}
+        for st, seq in base["streams"].items():
+            for pos, t in enumerate(seq):
+                k = (t["node"], t["tile"])
+                prio[k] = (schedule.ENGINES.index(st), pos)
+                before[k] = {tuple(w) for w in t["wait"]} | ({(seq[pos - 1]["node"], seq[pos - 1]["tile"])} if pos else set())
+        order = [(t["node"], t["tile"]) for t in schedule.serial_schedule(dag)["streams"]["aicore"]]
+        assert sorted(order) == sorted(prio)
+        done = set()
+        for k in order:
+            assert before[k] <= done
+            ready = [r for r in prio if r not in done and before[r] <= done]
+            assert prio[k] == min(prio[r] for r in ready)
+            done.add(k)
