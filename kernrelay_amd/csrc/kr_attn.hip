@@ -295,20 +295,38 @@ AttnKernel(AttnParams p)
     // returns the O rescale factor (1 unless the row max moved). The row max
     // is taken on raw scores, before scaling (scale > 0).
     auto softmax = [&](f32x16 (&sacc)[2], uint4 (&pf)[4]) -> float {
-        // max as a tree (short dependency chains)
+        // row max as a tree. Head size 128: 3-input steps in IEEE maximum
+        // (v_maximum3_f32 needs no quieting of its inputs, while fmaxf's
+        // maxnum first canonicalizes every MFMA result in IEEE mode: 18
+        // instructions per block instead of 46). Head size 64 keeps fmaxf,
+        // which measured faster there. Both equal on the finite and -inf
+        // scores here.
+        auto mx2 = [](float a, float b) {
+            if constexpr (D == 64) {
+                return fmaxf(a, b);
+            } else {
+                return __builtin_elementwise_maximum(a, b);
+            }
+        };
         float mx[4];
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
             const int kh = t >> 1, v0 = (t & 1) * 8;
-            mx[t] = fmaxf(fmaxf(fmaxf(sacc[kh][v0], sacc[kh][v0 + 1]), fmaxf(sacc[kh][v0 + 2], sacc[kh][v0 + 3])),
-                          fmaxf(fmaxf(sacc[kh][v0 + 4], sacc[kh][v0 + 5]), fmaxf(sacc[kh][v0 + 6], sacc[kh][v0 + 7])));
+            float x[8];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) x[e] = sacc[kh][v0 + e];
+            if constexpr (D == 64) {
+                mx[t] = mx2(mx2(mx2(x[0], x[1]), mx2(x[2], x[3])), mx2(mx2(x[4], x[5]), mx2(x[6], x[7])));
+            } else {
+                mx[t] = mx2(mx2(mx2(mx2(x[0], x[1]), x[2]), mx2(mx2(x[3], x[4]), x[5])), mx2(x[6], x[7]));
+            }
         }
-        float mloc = fmaxf(fmaxf(mx[0], mx[1]), fmaxf(mx[2], mx[3]));
+        float mloc = mx2(mx2(mx[0], mx[1]), mx2(mx[2], mx[3]));
         // lanes l and l ^ 32 hold the same query: v_permlane32_swap hands
         // every lane both halves' values (no LDS round trip)
         {
             const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mloc), __float_as_uint(mloc), false, false);
-            mloc = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1])) * p.scale_log2;
+            mloc = mx2(__uint_as_float(sw[0]), __uint_as_float(sw[1])) * p.scale_log2;
         }
         // lazy rescale: the row's reference max m moves only when a score
         // exceeds it by more than 2^8 (so p = 2^(s - m) <= 256, exact in
@@ -318,7 +336,7 @@ AttnKernel(AttnParams p)
         const float mnew = move ? mloc : m;
         const float msub = mnew == -INFINITY ? 0.0f : mnew;
         const float alpha = move ? __builtin_amdgcn_exp2f(m - msub) : 1.0f;
-        float ls[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+        float ls[4];
 #pragma unroll
         for (int c = 0; c < 4; ++c) {
             const int kh = c >> 1, vb = (c & 1) * 8;
@@ -326,7 +344,7 @@ AttnKernel(AttnParams p)
 #pragma unroll
             for (int e = 0; e < 8; ++e) {
                 pv[e] = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[kh][vb + e], p.scale_log2, -msub));
-                ls[e & 3] += pv[e];
+                ls[e & 3] = c == 0 && e < 4 ? pv[e] : ls[e & 3] + pv[e];
             }
             pf[c] = make_uint4(Pack2<DT>(pv[0], pv[1]), Pack2<DT>(pv[2], pv[3]), Pack2<DT>(pv[4], pv[5]),
                                Pack2<DT>(pv[6], pv[7]));
