@@ -61,15 +61,17 @@ def hf_config(model_dir):
     return Qwen2Config(**common), "qwen2"
 
 
-def hf_model(model_dir, dtype=torch.float32):
-    """transformers Qwen2/Qwen3ForCausalLM holding the model directory's weights."""
+def hf_model(model_dir, dtype=torch.float32, device="cpu"):
+    """transformers Qwen2/Qwen3ForCausalLM holding the model directory's
+    weights, built on `device` (a GPU builds a 7B model in seconds)."""
     cfg, kind = hf_config(model_dir)
     if kind == "qwen3":
         from transformers import Qwen3ForCausalLM as Cls
     else:
         from transformers import Qwen2ForCausalLM as Cls
     cfg._attn_implementation = "eager"
-    model = Cls(cfg).eval()
+    with torch.device(device):
+        model = Cls(cfg).eval()
     meta = _manifest(model_dir)
     raw = np.memmap(Path(model_dir) / "weights.bin", dtype=np.uint8, mode="r")
     sd = {}
@@ -92,7 +94,7 @@ def hf_model(model_dir, dtype=torch.float32):
     sd["model.norm.weight"] = _tensor(raw, meta, "final_norm.weight")
     if not cfg.tie_word_embeddings:
         sd["lm_head.weight"] = _tensor(raw, meta, "lm_head.weight_t").t()
-    sd = {k: v.to(dtype).contiguous() for k, v in sd.items()}
+    sd = {k: v.to(device=device, dtype=dtype).contiguous() for k, v in sd.items()}
     missing, unexpected = model.load_state_dict(sd, strict=False)
     missing = [m for m in missing if not (cfg.tie_word_embeddings and m == "lm_head.weight")]
     if missing or unexpected:
@@ -103,15 +105,20 @@ def hf_model(model_dir, dtype=torch.float32):
     return model.to(dtype)
 
 
-def last_logits(model_dir, dtype=torch.float32, threads=None):
-    """fp32 [V] last-token logits of the transformers model on ids.bin."""
+def last_logits(model_dir, dtype=torch.float32, threads=None, device="cpu"):
+    """fp32 [V] last-token logits (on the CPU) of the transformers model on
+    ids.bin, run on `device`. On a GPU keep dtype fp32: the eager attention
+    multiplies by a transposed key view, which this stack runs reliably in
+    fp32 only."""
     if threads:
         torch.set_num_threads(threads)
     ids = torch.from_numpy(np.fromfile(Path(model_dir) / "ids.bin", dtype=np.int64)).reshape(1, -1)
-    model = hf_model(model_dir, dtype)
+    model = hf_model(model_dir, dtype, device)
     with torch.no_grad():
-        out = model(input_ids=ids, use_cache=False, logits_to_keep=1)
-    return out.logits[0, -1].float()
+        out = model(input_ids=ids.to(device), use_cache=False, logits_to_keep=1)
+    last = out.logits[0, -1].float().cpu()
+    del model, out
+    return last
 
 
 def write_reference(model_dir, dtype=torch.float32):

@@ -15,6 +15,7 @@ no code with the oracle; the larger shapes use the oracle's files.
 """
 
 import os
+from pathlib import Path
 
 import numpy as np
 import pytest
@@ -256,3 +257,59 @@ def test_profile_many(gpu, tmp_path):
     got = {(c["op"], c["k"]) for c in r["cases"] if "best_us" in c}
     assert got == {(c["op"], c["k"]) for c in cases}
     assert all(c["best_us"] > 0 for c in r["cases"])
+
+
+def test_qwen25_7b_full_depth_vs_transformers(gpu, tmp_path):
+    """The benchmarked workload itself: the 28-layer Qwen2.5-7B-shaped model
+    that bench.py writes (seed 1234, weights generated on the GPU) at seq
+    2048, relay_split:4 and the serial program, against transformers'
+    Qwen2ForCausalLM holding the same weights in fp32 on the GPU (the role of
+    the reference's exporter, scripts/export_model.py:205-223). Asserts the
+    last-token argmax (129005 on MI355X) equals transformers' and that the
+    split is bit-identical to serial.
+
+    Measured deviation of our bf16 logits from transformers' fp32 ones: max
+    0.41, mean 0.075 (logits reach 5.2, spread ~1.2). That is what bf16
+    activations accumulate over 28 layers (~10 roundings each, a random walk
+    of sqrt(280) x 2^-8 ~ 6% of the hidden state); the two-layer tests at
+    these shapes hold 8e-2 against the oracle. The envelope asserted here is
+    max 0.6, mean 0.1. transformers' top-2 margin is 0.045, below the max
+    deviation; what decides the argmax is our deviation at transformers' top
+    logits, measured 0.004, 0.010 and 0.14 for the top three (reported by
+    the test)."""
+    import shutil
+    import tempfile
+
+    base = "/dev/shm" if os.path.isdir("/dev/shm") and shutil.disk_usage("/dev/shm").free > 40e9 else None
+    if base is None and shutil.disk_usage(tmp_path).free < 40e9:
+        pytest.skip("needs ~16 GB of free space for the 7B model directory")
+    tmp = Path(tempfile.mkdtemp(prefix="kr_7b_full_", dir=base))
+    try:
+        announce("write the bench's 7B model dir (28 layers, seq 2048, seed 1234, GPU-generated)")
+        d = modeldir.write_model_dir(tmp / "m", "qwen2.5-7b", seq=2048, device="cuda")
+        torch.cuda.synchronize()
+        torch.cuda.empty_cache()
+        got = {}
+        for mode in ("graph_whole", "relay_split:4"):
+            dump = tmp / ("dump_" + mode.replace(":", "_"))
+            dump.mkdir()
+            r = run(d, mode, 2048, dump, iters=1)
+            assert r["flag_timeouts"] == 0
+            w = np.fromfile(dump / "last_logits_bf16.bin", dtype=np.uint16)
+            got[mode] = (r, torch.from_numpy(w.view(np.int16).copy()).view(torch.bfloat16).double())
+        assert got["graph_whole"][0]["logits_fnv64"] == got["relay_split:4"][0]["logits_fnv64"]
+        torch.cuda.empty_cache()
+        announce("transformers Qwen2ForCausalLM fp32 on the GPU")
+        ref = hf.last_logits(d, torch.float32, device="cuda").double()
+        torch.cuda.empty_cache()
+        top = torch.topk(ref, 3)
+        g = got["relay_split:4"][1]
+        err = (g - ref).abs()
+        announce("transformers argmax %d (margin %.4g); ours %d; max |d| %.4g, mean %.4g; |d| at the top three %s" % (
+            int(top.indices[0]), float(top.values[0] - top.values[1]), int(g.argmax()), float(err.max()),
+            float(err.mean()), [round(float(err[i]), 4) for i in top.indices]))
+        assert int(g.argmax()) == int(top.indices[0])
+        assert got["relay_split:4"][0]["argmax"] == int(top.indices[0])
+        assert float(err.max()) <= 0.6 and float(err.mean()) <= 0.1, (float(err.max()), float(err.mean()))
+    finally:
+        shutil.rmtree(tmp, ignore_errors=True)
