@@ -283,8 +283,9 @@ def test_shipped_mi355x_costs_cover_the_7b_dag():
         assert key in costs.curves
     plan = P.plan_dag(dag, {"table": table["profile_table"]})
     sched = P.simulate(dag, costs)
-    # the cost file keeps k=1 times to 1 ns; the profile table unrounded
-    assert plan["base_makespan_us"] == pytest.approx(sched["makespan_us"], rel=1e-6)
+    # the cost file keeps k=1 times to 1 ns, the profile table unrounded:
+    # at most half a nanosecond per node of the DAG (all 28 layers' ops)
+    assert abs(plan["base_makespan_us"] - sched["makespan_us"]) <= 0.5e-3 * len(dag["nodes"])
     # serial lower bound: the aic queue alone
     aic = sum(costs.base(n) for n in dag["nodes"] if n["engine"] in ("aic", "aicore"))
     assert plan["base_makespan_us"] >= aic
