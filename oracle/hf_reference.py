@@ -121,15 +121,35 @@ def last_logits(model_dir, dtype=torch.float32, threads=None, device="cpu"):
     return last
 
 
-def write_reference(model_dir, dtype=torch.float32):
-    """Write ref_last_logits.bin and ref.json from transformers (the files
-    export_model.py:211-223 writes); returns the logits and their top-2."""
-    last = last_logits(model_dir, dtype)
+def write_reference(model_dir, dtype=torch.float32, device="cpu"):
+    """Write ref_last_logits.bin and ref.json from transformers run on
+    `device` (the files export_model.py:211-223 writes, which kr_qwen_run's
+    Verify compares against); returns the logits and their top-2."""
+    last = last_logits(model_dir, dtype, device=device)
     path = Path(model_dir)
     last.numpy().astype(np.float32).tofile(path / "ref_last_logits.bin")
     top = torch.topk(last, 2)
+    where = "GPU" if str(device).startswith("cuda") else "CPU"
     ref = {"argmax_last": int(top.indices[0]), "sum": float(last.sum()), "abs_mean": float(last.abs().mean()),
            "margin": float(top.values[0] - top.values[1]),
-           "source": "transformers %s %s CPU" % (hf_config(path)[1], str(dtype).replace("torch.", ""))}
+           "source": "transformers %s %s %s" % (hf_config(path)[1], str(dtype).replace("torch.", ""), where)}
     (path / "ref.json").write_text(json.dumps(ref, indent=1))
     return {"last_logits": last, "argmax": ref["argmax_last"], "margin": ref["margin"]}
+
+
+def main(argv=None):
+    """python -m oracle.hf_reference MODEL_DIR [--device cuda] [--dtype bf16]:
+    the reference step of the exporter for a model directory."""
+    import argparse
+    ap = argparse.ArgumentParser(description=main.__doc__)
+    ap.add_argument("model_dir")
+    ap.add_argument("--device", default="cpu")
+    ap.add_argument("--dtype", choices=("fp32", "bf16"), default="fp32")
+    args = ap.parse_args(argv)
+    r = write_reference(args.model_dir, torch.float32 if args.dtype == "fp32" else torch.bfloat16, args.device)
+    print(json.dumps({"argmax_last": r["argmax"], "margin": r["margin"]}))
+    return 0
+
+
+if __name__ == "__main__":
+    raise SystemExit(main())

@@ -279,8 +279,10 @@ def test_full_depth_vs_transformers(gpu, tmp_path, preset):
     layers, q/k-norm, seq 4096), serial and relay_split:4 (bit-identical),
     against transformers' Qwen2/Qwen3ForCausalLM holding the same weights in
     fp32 on the GPU (the role of the reference's exporter,
-    scripts/export_model.py:205-223). The last-token argmax must equal
-    transformers' (7B: 129005, the bench line's argmax).
+    scripts/export_model.py:205-223, whose files ref_last_logits.bin /
+    ref.json it writes for the runtime's own Verify to check, as
+    qwen_main.cpp does). The last-token argmax must equal transformers' (7B:
+    129005, the bench line's argmax).
 
     The deviation envelopes (FULL_DEPTH) are what bf16 activations
     accumulate over the layers: ~10 roundings a layer make a random walk of
@@ -302,6 +304,11 @@ def test_full_depth_vs_transformers(gpu, tmp_path, preset):
         d = modeldir.write_model_dir(tmp / "m", preset, seq=seq, device="cuda")
         torch.cuda.synchronize()
         torch.cuda.empty_cache()
+        # the exporter's reference step: transformers on the GPU writes
+        # ref_last_logits.bin / ref.json, which the runtime's Verify reads
+        announce("transformers %s fp32 on the GPU -> ref_last_logits.bin, ref.json" % preset)
+        ref = hf.write_reference(d, torch.float32, device="cuda")["last_logits"].double()
+        torch.cuda.empty_cache()
         got = {}
         for mode in ("graph_whole", "relay_split:4"):
             dump = tmp / ("dump_" + mode.replace(":", "_"))
@@ -312,11 +319,11 @@ def test_full_depth_vs_transformers(gpu, tmp_path, preset):
             got[mode] = (r, torch.from_numpy(w.view(np.int16).copy()).view(torch.bfloat16).double())
         assert got["graph_whole"][0]["logits_fnv64"] == got["relay_split:4"][0]["logits_fnv64"]
         assert got["relay_split:4"][0]["flag_edges"] > 0
-        torch.cuda.empty_cache()
-        announce("transformers %s fp32 on the GPU" % preset)
-        ref = hf.last_logits(d, torch.float32, device="cuda").double()
-        torch.cuda.empty_cache()
         top = torch.topk(ref, 3)
+        # the runtime's own Verify against the written reference
+        rv = got["relay_split:4"][0]
+        assert rv["ref_argmax"] == int(top.indices[0]) == rv["argmax"], (rv["ref_argmax"], rv["argmax"])
+        assert rv["maxdiff"] is not None and rv["maxdiff"] <= max_tol, rv["maxdiff"]
         g = got["relay_split:4"][1]
         err = (g - ref).abs()
         announce("transformers argmax %d (margin %.4g); ours %d; max |d| %.4g, mean %.4g; |d| at the top three %s" % (
