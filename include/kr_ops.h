@@ -164,7 +164,7 @@ int kr_op_gemm_streamk(int dtype, const void *A, int64_t lda, const void *Bt, in
  * kr_op_gemm_streamk; the counters are cleared at every call. Shapes whose
  * split needs more than the array holds fail with an error naming both
  * sizes. All calls on one GPU share the array: calls that may overlap in
- * time on one GPU (different streams, or hosts threads without ordering)
+ * time on one GPU (different streams, or host threads without ordering)
  * race and must not be issued. */
 int kr_op_gemm_streamk_noalloc(int dtype, const void *A, int64_t lda, const void *Bt, int64_t ldb, void *C,
                                int64_t ldc, const void *bias, int M, int N, int K, void *stream);
