@@ -95,7 +95,7 @@ def cpu_baseline(model_dir, seconds_hint=20):
     from oracle import ops as O
     from oracle import qwen as oq
 
-    # the CPU share this process may use (affinity), at most 16 on the GPU box
+    # the CPU share this process may use (affinity), at most 16 threads
     threads = max(1, min(16, len(os.sched_getaffinity(0))))
     torch.set_num_threads(threads)
     m = oq.ModelDir(model_dir)
@@ -240,8 +240,8 @@ def main():
         profile_consumers(args.reps)
         return
     if args.gpus != 1:
-        print("bench.py: this build targets one GPU; --gpus %d is not supported (the relay path is "
-              "single-device; see DESIGN.md for how it would shard)" % args.gpus, file=sys.stderr)
+        print("bench.py: --gpus %d is not supported: the relay path runs on one GPU (across GPUs it would "
+              "shard the sequence's rows, each GPU holding the weights)" % args.gpus, file=sys.stderr)
         sys.exit(2)
 
     import torch

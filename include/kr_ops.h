@@ -220,7 +220,7 @@ int kr_op_attention(int dtype, const void *q, int64_t ldq, const void *k, int64_
  * before the first call and left zero by every call; calls sharing them must
  * not overlap. Same role as kr_op_attention (reference
  * exec/qwen_main.cpp:591-614, FlashN); the split is a scheduling choice of
- * this build with no reference counterpart. */
+ * this library with no reference counterpart. */
 int kr_op_attention_workspace(int S, int HQ, int D, size_t *ws_bytes, int *counters);
 int kr_op_attention_split(int dtype, const void *q, int64_t ldq, const void *k, int64_t ldk,
                           const void *v, int64_t ldv, void *out, int64_t ldo, int S, int HQ, int HKV,

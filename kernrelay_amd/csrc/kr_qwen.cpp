@@ -294,7 +294,7 @@ public:
         r.Set("flag_timeouts", Value::MakeNumber(flag_timeouts_));
         r.Set("host_best_us", Value::MakeNumber(Min(host_samples_)));
         r.Set("host_typical_us", Value::MakeNumber(Median(host_samples_)));
-        // additions of this build
+        // fields beyond the reference's result keys
         r.Set("tiles", Value::MakeNumber(mode_.tiles));
         r.Set("device_best_us", Value::MakeNumber(Min(dev_samples_)));
         r.Set("device_typical_us", Value::MakeNumber(Median(dev_samples_)));

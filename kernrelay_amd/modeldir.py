@@ -22,17 +22,17 @@ from pathlib import Path
 import torch
 
 PRESETS = {
-    # BASELINE config 3
+    # Qwen2.5-0.5B shapes (tied lm_head)
     "qwen2.5-0.5b": dict(hidden_size=896, intermediate_size=4864, num_hidden_layers=24,
                          num_attention_heads=14, num_key_value_heads=2, head_dim=64, vocab_size=151936,
                          tie_word_embeddings=True, attention_bias=True, qk_norm=False,
                          rope_theta=1e6, rms_norm_eps=1e-6),
-    # BASELINE config 4 (headline)
+    # Qwen2.5-7B shapes (the benchmarked prefill)
     "qwen2.5-7b": dict(hidden_size=3584, intermediate_size=18944, num_hidden_layers=28,
                        num_attention_heads=28, num_key_value_heads=4, head_dim=128, vocab_size=152064,
                        tie_word_embeddings=False, attention_bias=True, qk_norm=False,
                        rope_theta=1e6, rms_norm_eps=1e-6),
-    # BASELINE config 5 (Qwen3-VL-8B language model shapes)
+    # Qwen3-8B text shapes (the Qwen3-VL-8B language model)
     "qwen3-8b": dict(hidden_size=4096, intermediate_size=12288, num_hidden_layers=36,
                      num_attention_heads=32, num_key_value_heads=8, head_dim=128, vocab_size=151936,
                      tie_word_embeddings=False, attention_bias=False, qk_norm=True,

@@ -1,7 +1,7 @@
 """CPU oracle for the KernRelay relay path — TEST INFRASTRUCTURE ONLY.
 
 Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may
-import this package, and only as the checker (or the timed CPU baseline),
+import this package, and only to check results (or as the timed CPU baseline),
 never as the thing measured or shipped. The product (kernrelay_amd/ and
 libkernrelay.so) never imports it.
 

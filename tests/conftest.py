@@ -23,7 +23,7 @@ def gpu_available():
 
 @pytest.fixture(scope="session")
 def gpu():
-    """Device guard for GPU tests: on a GPU box the library must load (no fallback)."""
+    """Device guard for GPU tests: with a GPU present the library must load (no fallback)."""
     if not gpu_available():
         pytest.skip("no GPU visible")
     from kernrelay_amd import libapi

@@ -16,7 +16,7 @@ Tolerances. transformers runs in fp32; the oracle rounds every stored
 activation to bf16 and uses the bf16 RoPE tables of the model directory, so
 the two differ by bf16 rounding noise, which grows with the activations:
   * default init (std 0.02, the init every GPU test uses): within the
-    north_star bound |d| <= 2e-2 + 1e-2 |ref| (measured 0.35 and 0.80 of it);
+    bf16 parity bound |d| <= 2e-2 + 1e-2 |ref| (measured 0.35 and 0.80 of it);
   * wide init (weights std 0.05, norm gains 1 + N(0, 0.3), so that a dropped
     or misplaced gain moves the logits): |d| <= 3e-2 max|ref| (measured 0.012
     and 0.015 of max|ref|), the same argmax.
