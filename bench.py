@@ -307,7 +307,8 @@ def main():
         dag = None
         if not args.no_dag:
             from kernrelay_amd import dag_bench
-            log("DAG workloads: tiny mm->GELU, 4096^3 mm -> {softmax, gelu, cast} at k=1,2,4,8")
+            log("DAG workloads: tiny mm->GELU, 4096^3 mm -> {softmax, gelu, cast} at k=1,2,4,8, the reference's "
+                "E3/E4 and two-wave DAGs")
             dag = dag_bench.run_all()
         cpu = None
         if not args.no_cpu:

@@ -1152,6 +1152,10 @@ private:
                 WaitLaunchMulti(wb, int(rows_a), int(in_rows), st.data(), int(st.size()), s);
                 LaunchConsumer(rc, L, s, rows_a, in_rows - rows_a, RelayWait{}, 0, RelayPub{});
             }
+            // a consumer that is itself a producer (mm -> GELU -> mm): its
+            // rows may span both launches, so it releases its tiles behind
+            // the last one (nothing when it publishes nothing)
+            for (int k = 0; k < L.merged; ++k) PublishLaunch(pub, k, s);
         }
         Check(hipGetLastError(), "task launch");
         if (L.publish && sync_ == "event" && events) Check(hipEventRecord(L.pub_event, s), "record event");

@@ -10,7 +10,10 @@
   softmax, cast, {GELU, softmax}) at its k, next to its published times;
   for an elementwise consumer also the in-register relay (the same split
   schedule with the consumer computed in the GEMM's epilogue,
-  KR_PLAN_EPILOGUE=1).
+  KR_PLAN_EPILOGUE=1);
+* the reference's two-wave DAGs on one device (two independent mm -> GELU
+  chains; mm -> GELU -> mm -> GELU) at k = 4 and 8, next to its published
+  times.
 
 Each variant runs as a replayed graph per stream (`graph_per_stream`); the
 reported time is the device makespan (HIP events on both streams, best and
@@ -151,6 +154,39 @@ def reference_e34(tmp, iters=20, warmup=3):
     return out
 
 
+# The reference's two-wave table (Ascend 910B3, nhp_exec, best of 3 x 5 runs):
+# case -> (dag, k, serial us, B0 us, split us), RESULTS.md:104-108.
+E9_REFERENCE = {
+    "e9_two_waves_k4": ("e9_two_waves", 4, 1791.2, 1617.6, 1532.0),
+    "e9_two_waves_k8": ("e9_two_waves", 8, 1840.9, 1648.0, 1571.4),
+    "e9_chain2_k4": ("e9_chain2", 4, 2270.1, 2276.0, 2063.6),
+    "e9_chain2_k8": ("e9_chain2", 8, 2275.8, 2290.0, 2105.0),
+}
+
+
+def reference_e9(tmp, iters=20, warmup=3):
+    """The reference's two-wave DAGs on one device at its shapes (fp16,
+    DetValue inputs, one rank): two independent mm -> GELU chains, and
+    mm -> GELU -> mm -> GELU; serial, B0 and the split at k, with the
+    reference's published times beside ours."""
+    out = {}
+    for case, (name, k, r_serial, r_b0, r_split) in E9_REFERENCE.items():
+        v = workloads.variants(workloads.e9_dag(name), k)
+        rs = {vn: _plan(v[vn], tmp, "%s_%s" % (case, vn), iters, warmup) for vn in ("serial", "b0", "split")}
+        ours = {vn: round(rs[vn]["device_best_us"], 2) for vn in rs}
+        out[case] = {
+            "k": k,
+            "serial_us": ours["serial"], "b0_us": ours["b0"], "split_us": ours["split"],
+            "serial_over_split": round(ours["serial"] / ours["split"], 4),
+            "b0_over_split": round(ours["b0"] / ours["split"], 4),
+            "flag_edges": rs["split"]["flag_edges"],
+            "reference_serial_over_split": round(r_serial / r_split, 4),
+            "reference_us": {"serial": r_serial, "b0": r_b0, "split": r_split},
+            "checksums_equal": len({rs[vn]["checksum"] for vn in rs}) == 1,
+        }
+    return out
+
+
 def _event_us(fn, reps=10):
     import torch
     fn()
@@ -193,7 +229,8 @@ def kernels_alone(M=4096, K=4096, N=4096):
 def run_all(iters=20):
     with tempfile.TemporaryDirectory(prefix="kr_dag_") as tmp:
         return {"tiny_mm_gelu": tiny(tmp), "fanout_4096": fanout(tmp, iters=iters),
-                "alone_4096": kernels_alone(), "reference_e34": reference_e34(tmp, iters=iters)}
+                "alone_4096": kernels_alone(), "reference_e34": reference_e34(tmp, iters=iters),
+                "reference_e9": reference_e9(tmp, iters=iters)}
 
 
 def main(argv=None):

@@ -79,6 +79,34 @@ def e34_dag(name, consumers, M=32768, K=1024, N=2048):
     return schedule.dag_from_dict({"name": name, "nodes": nodes, "edges": edges})
 
 
+def e9_dag(name, M=32768):
+    """The reference's two-wave DAGs on one device (dags/e9_two_waves.json,
+    dags/e9_chain2.json), fp16, DetValue inputs, 4 tiles by default:
+    e9_two_waves is two independent mm(32768x1024x2048) -> GELU chains;
+    e9_chain2 is mm(K=1024) -> GELU -> mm(K=2048) -> GELU, the second GEMM
+    reading the first GELU's output as its A operand."""
+    def mm(node, K):
+        return {"name": node, "op": "matmul", "engine": "aic", "shape": {"M": M, "K": K, "N": 2048},
+                "dtype": "fp16", "tiles": 4}
+
+    def gelu(node):
+        return {"name": node, "op": "gelu", "engine": "aiv", "shape": {"rows": M, "cols": 2048},
+                "dtype": "fp16", "tiles": 4}
+
+    def edge(src, dst):
+        return {"src": src, "dst": dst, "kind": "data"}
+
+    if name == "e9_two_waves":
+        nodes = [mm("mm1", 1024), gelu("gelu1"), mm("mm2", 1024), gelu("gelu2")]
+        edges = [edge("mm1", "gelu1"), edge("mm2", "gelu2")]
+    elif name == "e9_chain2":
+        nodes = [mm("mm1", 1024), gelu("gelu1"), mm("mm2", 2048), gelu("gelu2")]
+        edges = [edge("mm1", "gelu1"), edge("gelu1", "mm2"), edge("mm2", "gelu2")]
+    else:
+        raise ValueError("unknown one-device E9 DAG %r (e9_mixed needs an all-reduce)" % name)
+    return schedule.dag_from_dict({"name": name, "nodes": nodes, "edges": edges})
+
+
 def variants(dag, k, nranks=1):
     """serial (one stream), B0 (two streams, unsplit) and split-at-k schedules
     (the reference's E3/E4 variants, python/kernrelay/e34.py:16-22)."""

@@ -11,7 +11,7 @@ import torch
 from kernrelay_amd import libapi, schedule, workloads
 from oracle import dag_eval
 from tests.conftest import announce
-from tests.test_oracle_dag import KATS, kat_dag, ln_mm_dag, ref_dag
+from tests.test_oracle_dag import E9_KATS, KATS, kat_dag, ln_mm_dag, ref_dag
 
 pytestmark = pytest.mark.gpu
 
@@ -180,6 +180,44 @@ def test_reference_checksums_on_gpu(gpu, tmp_path, name, consumers, expected):
     assert r["_rc"] == 0 and r["ok"], r
     assert abs(r["checksum"] - expected) / abs(expected) < 1e-3, (r["checksum"], expected)
     assert abs(r["checksum"] - dag_eval.checksum(sched)) / abs(expected) < 1e-3
+
+
+@pytest.mark.parametrize("k", [4, 8])
+@pytest.mark.parametrize("name,expected,tol", E9_KATS)
+def test_e9_reference_checksums_on_gpu(gpu, tmp_path, name, expected, tol, k):
+    """The reference's two-wave DAGs at its shapes (fp16 GEMMs over 32768
+    rows, 2 ranks, DetValue inputs) split at k reproduce its recorded
+    checksums (results/final/e9_raw.json) within its consistency gate, and
+    the oracle's: two independent mm -> GELU chains, and mm -> GELU -> mm ->
+    GELU, whose second GEMM waits on the GELU's published row tiles."""
+    dag = workloads.e9_dag(name)
+    sched = schedule.build_fixed_schedule(dag, {n.name: k for n in dag.nodes}, nranks=2)
+    path = schedule.dump_schedule(sched, tmp_path / "e9.json")
+    announce("plan_run E9 %s k=%d" % (name, k))
+    r = libapi.plan_run(path, devices="0,0", mode="direct", iters=1, warmup=0, out_json=tmp_path / "e9_out.json")
+    assert r["_rc"] == 0 and r["ok"] and r["gate_timeouts"] == 0, r
+    ref = dag_eval.checksum(sched)
+    announce("checksum %.7f, recorded %.7f, oracle %.7f" % (r["checksum"], expected, ref))
+    assert abs(r["checksum"] - expected) / abs(expected) < 1e-3, (r["checksum"], expected)
+    assert abs(r["checksum"] - ref) / abs(expected) < 1e-3, (r["checksum"], ref)
+
+
+@pytest.mark.parametrize("name", ["e9_two_waves", "e9_chain2"])
+def test_e9_variants_bit_exact(gpu, tmp_path, name):
+    """The two-wave DAGs at 4096 rows: B0 and the relay split at k = 4 and 8
+    (graph per stream, device flags) store every node's output bit for bit
+    as the serial program does; the first 256 rows of every node against
+    the oracle."""
+    dag = workloads.e9_dag(name, M=4096)
+    _, base = run(schedule.serial_schedule(dag), tmp_path, "serial", iters=1, warmup=0)
+    for vn, k in (("b0", 1), ("split", 4), ("split", 8)):
+        r, outs = run(workloads.variants(dag, k)[vn], tmp_path, "%s%d" % (vn, k), mode="graph_per_stream")
+        assert r["ok"] and r["gate_timeouts"] == 0, r
+        if vn == "split":
+            assert r["flag_edges"] > 0
+        for node in base:
+            assert np.array_equal(base[node], outs[node]), (vn, k, node)
+    assert_close_to_oracle(schedule.serial_schedule(dag), base, rows=256)
 
 
 @pytest.mark.parametrize("k", [1, 2, 4, 8])

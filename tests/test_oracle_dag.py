@@ -41,6 +41,21 @@ def kat_dag(name, consumers):
     return ln_mm_dag() if consumers is None else ref_dag(name, consumers)
 
 
+# The reference's two-wave DAGs on one device (results/final/e9_raw.json:
+# the same checksum for serial, B0 and the split at k = 4 and 8; fp16, 2
+# ranks, DetValue inputs), with the bound each is held to. e9_chain2's
+# second GEMM reads GELU outputs over K = 2048: the oracle's checksum
+# (1.6084236, unchanged with fp64 accumulation) sits 1.2e-5 from the
+# recorded 1.608412 — one fp16 rounding step of a value near 0.02 among the
+# 32768 words summed, the reference's closed fp16 GEMM rounding a product
+# the other way. A wrong edge moves it by far more (mm2 reading mm1's
+# output: 2.474; mm2 on its own inputs: 5.663; one rank: 0.273).
+E9_KATS = [
+    ("e9_two_waves", 3.429432, 1.5e-6),
+    ("e9_chain2", 1.608412, 2e-5),
+]
+
+
 @pytest.mark.parametrize("name,consumers,expected", KATS)
 def test_reference_checksums(name, consumers, expected):
     dag = kat_dag(name, consumers)
@@ -91,3 +106,15 @@ def test_bf16_rounding_helper():
     # ties to even: 1 + 2^-8 -> 1.0, 1 + 3*2^-8 -> 1 + 2^-6
     assert back[0] == 1.0 and back[1] == 1.0 and back[2] == 1.0 + 2 ** -6
     assert back[3] == -2.5 and np.isinf(back[5])
+
+
+@pytest.mark.parametrize("name,expected,tol", E9_KATS)
+def test_e9_reference_checksums(name, expected, tol):
+    """Two independent mm -> GELU chains, and mm -> GELU -> mm -> GELU (a GEMM
+    consuming a GELU producer's rows), split at k=4 over 2 ranks, reproduce
+    the reference's recorded checksums."""
+    dag = workloads.e9_dag(name)
+    sched = schedule.build_fixed_schedule(dag, {n.name: 4 for n in dag.nodes}, nranks=2)
+    got = dag_eval.checksum(sched)
+    assert abs(got - expected) <= tol, (name, got, expected)
+    assert dag_eval.checksum(schedule.serial_schedule(dag, nranks=2)) == got
