@@ -205,18 +205,23 @@ def test_e9_reference_checksums_on_gpu(gpu, tmp_path, name, expected, tol, k):
 @pytest.mark.parametrize("name", ["e9_two_waves", "e9_chain2"])
 def test_e9_variants_bit_exact(gpu, tmp_path, name):
     """The two-wave DAGs at 4096 rows: B0 and the relay split at k = 4 and 8
-    (graph per stream, device flags) store every node's output bit for bit
-    as the serial program does; the first 256 rows of every node against
-    the oracle."""
+    (graph per stream, device flags), and the k = 4 split in the other
+    executor modes (direct launches with flags or events, graph_segment),
+    store every node's output bit for bit as the serial program does; the
+    first 256 rows of every node against the oracle."""
     dag = workloads.e9_dag(name, M=4096)
     _, base = run(schedule.serial_schedule(dag), tmp_path, "serial", iters=1, warmup=0)
-    for vn, k in (("b0", 1), ("split", 4), ("split", 8)):
-        r, outs = run(workloads.variants(dag, k)[vn], tmp_path, "%s%d" % (vn, k), mode="graph_per_stream")
-        assert r["ok"] and r["gate_timeouts"] == 0, r
-        if vn == "split":
+    cases = [("b0", 1, "graph_per_stream", None), ("split", 4, "graph_per_stream", None),
+             ("split", 8, "graph_per_stream", None), ("split", 4, "direct", None),
+             ("split", 4, "direct", {"KR_SYNC": "event"}), ("split", 4, "graph_segment", None)]
+    for vn, k, mode, env in cases:
+        tag = "%s%d_%s%s" % (vn, k, mode, "_event" if env else "")
+        r, outs = run(workloads.variants(dag, k)[vn], tmp_path, tag, mode=mode, env=env)
+        assert r["ok"] and r["gate_timeouts"] == 0, (tag, r)
+        if vn == "split" and r["sync"] == "flag":
             assert r["flag_edges"] > 0
         for node in base:
-            assert np.array_equal(base[node], outs[node]), (vn, k, node)
+            assert np.array_equal(base[node], outs[node]), (tag, node)
     assert_close_to_oracle(schedule.serial_schedule(dag), base, rows=256)
 
 
