@@ -24,7 +24,7 @@ Also reported: the producer GEMM alone (MFMA fraction of the 2.5 PFLOP/s
 bf16 peak) and each consumer alone (GB/s of its algorithmic read + write
 bytes against 8 TB/s).
 
-    python -m kernrelay_amd.dag_bench [--iters 20]
+    python -m kernrelay_amd.dag_bench [--iters 20] [--only reference_e9,...]
 """
 
 import argparse
@@ -226,18 +226,28 @@ def kernels_alone(M=4096, K=4096, N=4096):
     return out
 
 
-def run_all(iters=20):
+SECTIONS = ("tiny_mm_gelu", "fanout_4096", "alone_4096", "reference_e34", "reference_e9")
+
+
+def run_all(iters=20, only=SECTIONS):
     with tempfile.TemporaryDirectory(prefix="kr_dag_") as tmp:
-        return {"tiny_mm_gelu": tiny(tmp), "fanout_4096": fanout(tmp, iters=iters),
-                "alone_4096": kernels_alone(), "reference_e34": reference_e34(tmp, iters=iters),
-                "reference_e9": reference_e9(tmp, iters=iters)}
+        run = {"tiny_mm_gelu": lambda: tiny(tmp), "fanout_4096": lambda: fanout(tmp, iters=iters),
+               "alone_4096": kernels_alone, "reference_e34": lambda: reference_e34(tmp, iters=iters),
+               "reference_e9": lambda: reference_e9(tmp, iters=iters)}
+        return {name: run[name]() for name in SECTIONS if name in only}
 
 
 def main(argv=None):
     ap = argparse.ArgumentParser()
     ap.add_argument("--iters", type=int, default=20)
+    ap.add_argument("--only", default=",".join(SECTIONS),
+                    help="comma-separated sections to run (default: all): " + ", ".join(SECTIONS))
     args = ap.parse_args(argv)
-    print(json.dumps(run_all(args.iters)), flush=True)
+    only = [x for x in args.only.split(",") if x]
+    unknown = set(only) - set(SECTIONS)
+    if unknown:
+        raise SystemExit("unknown section(s): %s" % ", ".join(sorted(unknown)))
+    print(json.dumps(run_all(args.iters, only)), flush=True)
     return 0
 
 
