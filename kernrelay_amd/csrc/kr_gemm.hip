@@ -1015,6 +1015,53 @@ void GemmStreamKNeeds(int M, int N, int K, size_t *ws_bytes, int *counters)
     }
 }
 
+// Wave tail of a plain data-parallel 256x256 grid (the 8-wave staged kernel,
+// no relay, no RoPE / norm / unary epilogue, no forced tile): when its tiles
+// are not a whole number of rounds on the device, the last round runs partly
+// idle (gate/up 2048x37888: 1184 tiles = 4 rounds + 160). Then the columns
+// that fill whole rounds stay one launch (a), and the rest run as a second
+// launch (b) of 192x256 tiles, one round of three-quarter tiles instead of a
+// full round. Every tile shape runs the same MFMA over the same k16 chunks
+// in the same order: the same bits. The SwiGLU epilogue splits with C (its
+// gate/up groups of 8 never straddle a 256-column boundary).
+// KR_GEMM_TAIL=0 keeps one launch.
+bool SplitWaveTail(const GemmDesc &d, GemmDesc &a, GemmDesc &b)
+{
+    static const bool on = [] {
+        const char *e = std::getenv("KR_GEMM_TAIL");
+        return e == nullptr || std::atoi(e) != 0;
+    }();
+    if (!on || d.bm != 0 || d.bn != 0 || d.coresident || d.order_rows != 0) return false;
+    if (d.pub.ctrl != nullptr || d.wait.ctrl != nullptr || d.tail_act != nullptr || d.y != nullptr ||
+        d.rope_cos != nullptr || d.norm_y != nullptr)
+        return false;
+    if (d.K % kPipeK != 0 || ForceSimple() || MainLoopMode() != 2 || PipeWaves() != 8) return false;
+    const GemmTile t = GemmPickTile(d.M, d.N, 0, false);
+    if (t.bm != 256 || t.bn != 256) return false;
+    StreamKPlan skp;
+    if (d.streamk && PlanStreamK(d.M, d.N, d.K, skp)) return false;
+    const int64_t cus = CuCount();
+    const int64_t tm = (d.M + 255) / 256, tn = (d.N + 255) / 256;
+    const int64_t rounds = tm * tn / cus;
+    if (rounds < 1 || (tm * tn) % cus == 0 || (rounds * cus) % tm != 0) return false;
+    const int64_t n1 = rounds * cus / tm * 256;  // columns of the whole rounds
+    const int64_t n2 = d.N - n1;
+    if (n2 <= 0 || ((d.M + 191) / 192) * ((n2 + 255) / 256) > cus) return false;
+    a = d;
+    b = d;
+    a.N = int(n1);
+    a.bm = 256;
+    a.bn = 256;
+    b.N = int(n2);
+    b.bm = 192;
+    b.bn = 256;
+    b.Bt = static_cast<const uint16_t *>(d.Bt) + n1 * d.ldb;
+    if (d.C != nullptr) b.C = static_cast<uint16_t *>(d.C) + n1;
+    if (d.bias != nullptr) b.bias = static_cast<const uint16_t *>(d.bias) + n1;
+    if (d.epi_act != nullptr) b.epi_act = static_cast<uint16_t *>(d.epi_act) + n1 / 2;
+    return true;
+}
+
 void GemmLaunch(const GemmDesc &d, hipStream_t stream)
 {
     if (d.K % 8 != 0) throw std::runtime_error("gemm: K must be a multiple of 8");
@@ -1022,6 +1069,14 @@ void GemmLaunch(const GemmDesc &d, hipStream_t stream)
     if ((reinterpret_cast<uintptr_t>(d.A) | reinterpret_cast<uintptr_t>(d.Bt)) & 15)
         throw std::runtime_error("gemm: A/Bt must be 16-byte aligned");
     if ((d.lda | d.ldb) % 8 != 0) throw std::runtime_error("gemm: lda/ldb must be multiples of 8");
+    {
+        GemmDesc a, b;
+        if (SplitWaveTail(d, a, b)) {
+            GemmLaunch(a, stream);
+            GemmLaunch(b, stream);
+            return;
+        }
+    }
     GemmParams p{};
     p.A = static_cast<const uint16_t *>(d.A);
     p.Bt = static_cast<const uint16_t *>(d.Bt);
@@ -1125,7 +1180,7 @@ void GemmLaunch(const GemmDesc &d, hipStream_t stream)
     if (d.epi_act != nullptr && t.bn < 256) t = {t.bm >= 256 ? 256 : 128, 256};  // the epilogue pairs 16-col groups
     // 192x256 runs only on the staged 8-wave kernel; elsewhere 256x256 (the
     // same MFMA and K order: the same bits)
-    if (t.bm == 192 && (d.K % kPipeK != 0 || ForceSimple() || MainLoopMode() != 2 || d.epi_act != nullptr ||
+    if (t.bm == 192 && (d.K % kPipeK != 0 || ForceSimple() || MainLoopMode() != 2 ||
                         d.tail_act != nullptr || d.pub.ctrl != nullptr || d.wait.ctrl != nullptr))
         t = {256, 256};
     const bool bf = d.dtype == kBF16;

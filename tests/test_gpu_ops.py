@@ -462,6 +462,41 @@ def test_relay_wait_bound_reports_timeout(gpu):
     assert int(blk[0, 2]) == 1 and int(blk[0, 1]) == 2 and int(blk[0, 0]) == 2
 
 
+@pytest.mark.parametrize("M,N,K", [(2048, 37888, 3584), (2048, 152064, 3584), (1000, 37888, 512)])
+def test_gemm_wave_tail_split_bit_exact(gpu, M, N, K):
+    """A 256x256 grid that is not a whole number of rounds on the device runs
+    the columns of its partial last round as a second launch of 192x256
+    tiles (gate/up 2048x37888: 1184 tiles = 4 rounds + 160; lm_head
+    2048x152064: 18 rounds + 144; a ragged M of 1000). The product equals
+    the single-launch grid (a forced 256-row tile, never split) bit for bit,
+    the SwiGLU epilogue's act equals the standalone kernel on that product,
+    and nothing outside C or act is written."""
+    announce("gemm wave-tail split %dx%dx%d" % (M, N, K))
+    g = torch.Generator(device="cuda").manual_seed(M + N + K)
+    A = torch.randn(M, K, device="cuda", generator=g).to(torch.bfloat16)
+    Bt = (torch.randn(N, K, device="cuda", generator=g) * 0.02).to(torch.bfloat16)
+    ref = torch.empty(M, N, dtype=torch.bfloat16, device="cuda")
+    ops.gemm(A, Bt, ref, bm=256)
+    pad = torch.full((M + 8, N + 16), 7.0, dtype=torch.bfloat16, device="cuda")
+    C = pad[:M, :N]
+    ops.gemm(A, Bt, C)
+    torch.cuda.synchronize()
+    assert torch.equal(C, ref)
+    assert bool(torch.all(pad[M:] == 7.0)) and bool(torch.all(pad[:, N:] == 7.0))
+    del pad, C
+    if N > 40000:
+        return
+    I = N // 2
+    ref_a = torch.empty(M, I, dtype=torch.bfloat16, device="cuda")
+    ops.elementwise("swiglu_gu", ref, ref_a, rows=M, cols=I)
+    apad = torch.full((M + 8, I + 16), 7.0, dtype=torch.bfloat16, device="cuda")
+    act = apad[:M, :I]
+    ops.gemm_swiglu_epilogue(A, Bt, act)
+    torch.cuda.synchronize()
+    assert torch.equal(act, ref_a)
+    assert bool(torch.all(apad[M:] == 7.0)) and bool(torch.all(apad[:, I:] == 7.0))
+
+
 @pytest.mark.parametrize("M,I,K", [(1024, 1536, 512), (300, 512, 256), (2048, 4864, 896)])
 def test_gemm_swiglu_epilogue_bit_exact(gpu, M, I, K):
     """SwiGLU applied in the gate/up GEMM's epilogue (the in-register relay)
