@@ -39,8 +39,8 @@ def log(msg):
 # what the same counter reads for a plain 512 MiB device copy; and rocprof's
 # MFMA utilisation of the same launches (SQ_VALU_MFMA_BUSY_CYCLES over
 # GRBM_GUI_ACTIVE x SIMDs, at the clock the card ran).
-GATE_UP_TRAFFIC_BYTES = (408696.2 * 2.0 + 75776.0 * 1.0) * 1024
-GATE_UP_MFMA_UTIL = 0.633
+GATE_UP_TRAFFIC_BYTES = (423136.0 * 2.0 + 75776.0 * 1.0) * 1024
+GATE_UP_MFMA_UTIL = 0.635
 GATE_UP_TRAFFIC_SOURCE = "profiles/gemm_gate_up_swiglu_2048x37888x3584.md"
 
 
@@ -64,10 +64,11 @@ def gemm_roofline(run, serial, S, N, K):
             "traffic": round(GATE_UP_TRAFFIC_BYTES) if measured else None,
             "traffic_algorithmic": 2 * (S * K + N * K + S * N // 2),
             "traffic_source": GATE_UP_TRAFFIC_SOURCE if measured else None,
-            "kernel": "GemmPipeKernel<bf16,256,256,8 waves> gate/up projection %dx%dx%d, SwiGLU epilogue"
+            "kernel": "GemmPipeKernel<bf16,256,256,8 waves> + its 192x256 wave-tail launch, gate/up projection "
+                      "%dx%dx%d, SwiGLU epilogue"
                       % (S, N, K),
             "avg_launch_us": round(avg_us, 2), "launches": int(run["gate_up_launches"]),
-            "timing": "HIP events around each launch in an eager pass of the relay-split prefill",
+            "timing": "HIP events around each gate/up GEMM (its launches) in an eager pass of the relay-split prefill",
             "mfma_util_rocprof": GATE_UP_MFMA_UTIL if measured else None,
             "serial_gate_up": {"avg_launch_us": round(ser_us, 2),
                                "achieved": round(flops / (ser_us * 1e-6) / 1e12, 1),
