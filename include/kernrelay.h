@@ -35,8 +35,9 @@ const char *kr_version(void);
  *   iters/warmup  : timed and untimed executions
  *   devices       : "0" or "0,0" (one entry per rank; every rank runs on the
  *                   listed device); NULL/"" = device 0 for every rank
- *   mode          : "direct" | "graph" | "graph_per_stream"
- *                   ("graph_segment" is rejected: not built)
+ *   mode          : "direct" | "graph" | "graph_per_stream" | "graph_segment"
+ *                   (graph_segment: one graph per run of a lane between
+ *                   cross-lane waits, the segments joined by events)
  *   out_json      : path that receives the result JSON
  * Returns 0 on success; 2 for NULL arguments or usage errors; 1 on any other
  * failure (message on stderr).
@@ -50,8 +51,12 @@ int kr_plan_run(const char *schedule_json, int iters, int warmup,
  * (manifest.json + weights.bin + ids.bin [+ ref_last_logits.bin, ref.json]).
  * mode: serial | serial_fused | serial_graph | graph_whole |
  *       relay_event | relay_flag | relay_flag_graph |
- *       relay_split | relay_split:<k>        (row-tiled relay, k in 1..8,
- *                                             default 4; graph-replayed)
+ *       relay_split | relay_split:<k> | relay_split:<k>:<edges>
+ *         (row-tiled relay, k in 1..8, default 4; graph-replayed; edges =
+ *          o+down | o | down | none names the flag edges o -> Add+RMSNorm
+ *          and down -> Add+RMSNorm; default: every edge whose relay tiles
+ *          fit the device; the gate/up GEMM always hands SwiGLU its tiles
+ *          in its epilogue)
  * Result JSON keys follow reference exec/qwen_main.cpp:1785-1803.
  * Returns 0 on success; 1 with {"error":...} in `out` on failure.
  * Replaces reference exec/qwen_main.cpp:2287-2314.

@@ -97,8 +97,9 @@ void GemmLaunch(const GemmDesc &d, hipStream_t stream);
 
 // True when GemmLaunch can run the Add+RMSNorm relay consumer for this shape
 // and relay tile (rows_per_tile): a one-wave row width, whole tiles, and the
-// producer workgroups of one relay tile resident at once.
-bool GemmNormRelayFits(int M, int N, int K, int rows_per_tile, bool streamk_ws);
+// producer workgroups of one relay tile resident at once (device slots from
+// the occupancy of the kernel instantiation the launch runs).
+bool GemmNormRelayFits(int M, int N, int K, int rows_per_tile, bool streamk_ws, int dtype = kBF16);
 
 // Workspace a stream-K launch of this shape needs (0 bytes, 0 counters: the
 // launch runs data-parallel).

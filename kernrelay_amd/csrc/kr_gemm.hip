@@ -785,19 +785,97 @@ int CuCount()
     return v;
 }
 
+using GemmFn = void (*)(GemmParams);
+
+// The kernel a launch of BM x BN tiles runs over K, and its block size: the
+// 8-wave staged kernel for 192x256; for 256x256 the 8-wave kernel (stream-K
+// or data-parallel) unless KR_GEMM_WAVES=4; the 4-wave pipelined kernel for
+// the other tiles; the simple kernel where K % 64 != 0 or KR_GEMM_SIMPLE=1.
+template <int DT, int BM, int BN>
+GemmFn PickGemmKernel(int K, bool sk, int &threads)
+{
+    if constexpr (BM == 192) {
+        // 192x256: the 8-wave staged kernel only (GemmLaunch picks this tile
+        // only where that kernel runs)
+        static_assert(BN == 256, "192-row tiles pair with 256 columns");
+        if (sk || K % kPipeK != 0 || ForceSimple() || MainLoopMode() != 2)
+            throw std::logic_error("gemm: 192x256 tiles run the staged kernel only");
+        threads = 512;
+        return GemmPipeKernel<DT, BM, BN, 0, 8, false, 2>;
+    } else {
+        if (K % kPipeK == 0 && !ForceSimple()) {
+            if constexpr (BM == 256 && BN == 256) {
+                if (sk) {
+                    threads = 512;
+                    return MainLoopMode() == 2 ? GemmPipeKernel<DT, BM, BN, 0, 8, true, 2>
+                                               : GemmPipeKernel<DT, BM, BN, 0, 8, true>;
+                }
+                if (PipeWaves() == 8) {
+                    threads = 512;
+                    return MainLoopMode() == 2 ? GemmPipeKernel<DT, BM, BN, 0, 8, false, 2>
+                                               : GemmPipeKernel<DT, BM, BN, 0, 8>;
+                }
+            }
+            threads = kThreads;
+            switch (PrefetchStages()) {
+            case 2: return GemmPipeKernel<DT, BM, BN, 2, 4>;
+            case 4: return GemmPipeKernel<DT, BM, BN, 4, 4>;
+            default: return GemmPipeKernel<DT, BM, BN, 0, 4>;
+            }
+        }
+        threads = kThreads;
+        return GemmKernel<DT, BM, BN>;
+    }
+}
+
+// Workgroups of that kernel one CU holds at once, from the runtime's
+// occupancy query on the exact instantiation (registers, LDS, waves);
+// cached per (dtype, tile, K-path, stream-K).
+template <int DT, int BM, int BN>
+int GemmWgsPerCu(int K, bool sk)
+{
+    static int cache[2][2] = {{-1, -1}, {-1, -1}};
+    int &c = cache[K % kPipeK == 0 ? 1 : 0][sk ? 1 : 0];
+    if (c < 0) {
+        int threads = 0;
+        const GemmFn fn = PickGemmKernel<DT, BM, BN>(K, sk, threads);
+        int n = 0;
+        Check(hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, reinterpret_cast<const void *>(fn), threads, 0),
+              "gemm occupancy");
+        if (n < 1) throw std::runtime_error("gemm: kernel does not fit a CU");
+        c = n;
+    }
+    return c;
+}
+
+int GemmWgsPerCu(int dt, int bm, int bn, int K, bool sk)
+{
+    const bool bf = dt == kBF16;
+#define KR_OCC_CASE(BM_, BN_) \
+    if (bm == BM_ && bn == BN_) return bf ? GemmWgsPerCu<kBF16, BM_, BN_>(K, sk) : GemmWgsPerCu<kF16, BM_, BN_>(K, sk);
+    KR_OCC_CASE(256, 256)
+    KR_OCC_CASE(192, 256)
+    KR_OCC_CASE(256, 128)
+    KR_OCC_CASE(128, 256)
+    KR_OCC_CASE(128, 128)
+    KR_OCC_CASE(64, 256)
+#undef KR_OCC_CASE
+    throw std::runtime_error("gemm: unsupported tile " + std::to_string(bm) + "x" + std::to_string(bn));
+}
+
 // The Add+RMSNorm relay consumer waits inside the producer's workgroups for
 // the other producer workgroups of its relay tile. Workgroups are dispatched
 // in id order (per XCD) and a relay tile's are consecutive ids, so the waits
 // always end when a relay tile's workgroups fit the device at once: then
 // every earlier tile's workgroups are resident or finished. A stream-K grid
-// is resident as a whole (one workgroup per CU).
-bool NormRelayResident(int bm, int bn, int M, int N, int rows_per_tile, int sk_wgs)
+// must be resident as a whole. The device's slots come from the occupancy of
+// the kernel the launch runs.
+bool NormRelayResident(int dt, int bm, int bn, int M, int N, int K, int rows_per_tile, int sk_wgs)
 {
-    if (sk_wgs > 0) return sk_wgs <= CuCount();
+    if (sk_wgs > 0) return sk_wgs <= CuCount() * GemmWgsPerCu(dt, 256, 256, K, true);
     if (rows_per_tile <= 0 || rows_per_tile % bm != 0 || M % rows_per_tile != 0) return false;
     const int per = (rows_per_tile / bm) * ((N + bn - 1) / bn);
-    const int slots = CuCount() * (bm * bn >= 256 * 128 ? 1 : 2);
-    return per <= slots;
+    return per <= CuCount() * GemmWgsPerCu(dt, bm, bn, K, false);
 }
 
 // Stream-K plan of a GEMM whose data-parallel tiling leaves CUs idle.
@@ -877,13 +955,13 @@ void LaunchTyped(const GemmParams &base, int order_rows, int tail_tiles, hipStre
     if (p.rn_y != nullptr) {
         if (sk == nullptr && p.order_rows != p.pub.rows_per_tile)
             throw std::runtime_error("gemm: the Add+RMSNorm relay consumer needs the default relay-tile order");
-        if (!NormRelayResident(BM, BN, p.M, p.N, p.pub.rows_per_tile, sk != nullptr ? sk->G : 0))
+        if (!NormRelayResident(DT, BM, BN, p.M, p.N, p.K, p.pub.rows_per_tile, sk != nullptr ? sk->G : 0))
             throw std::runtime_error("gemm: a relay tile's producer workgroups do not fit the device at once; "
                                      "the Add+RMSNorm relay consumer would wait on workgroups not yet placed");
         // a grid resident as a whole releases every tile at about the same
         // time whatever the order: keep the grouped raster (square patches
         // per XCD, less operand traffic than relay-tile order)
-        if (sk == nullptr && p.gemm_wgs <= CuCount() * (BM * BN >= 256 * 128 ? 1 : 2)) p.order_rows = 0;
+        if (sk == nullptr && p.gemm_wgs <= CuCount() * GemmWgsPerCu<DT, BM, BN>(p.K, false)) p.order_rows = 0;
     }
     if (sk != nullptr) {
         if (BM != 256 || BN != 256 || sk->tiles != p.gemm_wgs) throw std::logic_error("gemm: stream-K plan mismatch");
@@ -897,39 +975,10 @@ void LaunchTyped(const GemmParams &base, int order_rows, int tail_tiles, hipStre
         grid_x += tail_tiles * p.tail_wpt;
     }
     const dim3 grid(grid_x);
-    if constexpr (BM == 192) {
-        // 192x256: the 8-wave staged kernel only (GemmLaunch picks this tile
-        // only where that kernel runs)
-        static_assert(BN == 256, "192-row tiles pair with 256 columns");
-        if (sk != nullptr || p.K % kPipeK != 0 || ForceSimple() || MainLoopMode() != 2)
-            throw std::logic_error("gemm: 192x256 tiles run the staged kernel only");
-        hipLaunchKernelGGL((GemmPipeKernel<DT, BM, BN, 0, 8, false, 2>), grid, dim3(512), 0, stream, p);
-        Check(hipGetLastError(), "gemm launch");
-        return;
-    } else if (p.K % kPipeK == 0 && !ForceSimple()) {
-        if constexpr (BM == 256 && BN == 256) {
-            if (sk != nullptr) {
-                if (MainLoopMode() == 2) hipLaunchKernelGGL((GemmPipeKernel<DT, BM, BN, 0, 8, true, 2>), grid, dim3(512), 0, stream, p);
-                else hipLaunchKernelGGL((GemmPipeKernel<DT, BM, BN, 0, 8, true>), grid, dim3(512), 0, stream, p);
-                Check(hipGetLastError(), "gemm launch");
-                return;
-            }
-            if (PipeWaves() == 8) {
-                if (MainLoopMode() == 2) hipLaunchKernelGGL((GemmPipeKernel<DT, BM, BN, 0, 8, false, 2>), grid, dim3(512), 0, stream, p);
-                else hipLaunchKernelGGL((GemmPipeKernel<DT, BM, BN, 0, 8>), grid, dim3(512), 0, stream, p);
-                Check(hipGetLastError(), "gemm launch");
-                return;
-            }
-        }
-        switch (PrefetchStages()) {
-        case 2: hipLaunchKernelGGL((GemmPipeKernel<DT, BM, BN, 2, 4>), grid, dim3(kThreads), 0, stream, p); break;
-        case 4: hipLaunchKernelGGL((GemmPipeKernel<DT, BM, BN, 4, 4>), grid, dim3(kThreads), 0, stream, p); break;
-        default: hipLaunchKernelGGL((GemmPipeKernel<DT, BM, BN, 0, 4>), grid, dim3(kThreads), 0, stream, p); break;
-        }
-    } else {
-        hipLaunchKernelGGL((GemmKernel<DT, BM, BN>), grid, dim3(kThreads), 0, stream, p);
-    }
-    Check(hipGetLastError(), "gemm launch");
+    int threads = 0;
+    const GemmFn fn = PickGemmKernel<DT, BM, BN>(p.K, sk != nullptr, threads);
+    void *args[] = {&p};
+    Check(hipLaunchKernel(reinterpret_cast<const void *>(fn), grid, dim3(threads), args, 0, stream), "gemm launch");
 }
 
 }  // namespace
@@ -988,19 +1037,20 @@ GemmTile GemmPickTile(int M, int N, int relay_rows, bool coresident)
     return best.bm < 0 ? best : pick192(best);
 }
 
-bool GemmNormRelayFits(int M, int N, int K, int rows_per_tile, bool streamk_ws)
+bool GemmNormRelayFits(int M, int N, int K, int rows_per_tile, bool streamk_ws, int dtype)
 {
     if (AddRmsNormRowCpl(N) == 0 || rows_per_tile <= 0 || M % rows_per_tile != 0) return false;
     StreamKPlan skp;
     const bool sk_pub_ok = rows_per_tile % 256 == 0 || 256 % rows_per_tile == 0;
-    if (streamk_ws && sk_pub_ok && !ForceSimple() && PlanStreamK(M, N, K, skp)) return skp.G <= CuCount();
+    if (streamk_ws && sk_pub_ok && !ForceSimple() && PlanStreamK(M, N, K, skp))
+        return NormRelayResident(dtype, 256, 256, M, N, K, rows_per_tile, skp.G);
     GemmTile t = GemmPickTile(M, N, rows_per_tile, false);
     if (const char *e = std::getenv("KR_GEMM_TILE")) {
         int bm = 0, bn = 0;
         if (std::sscanf(e, "%dx%d", &bm, &bn) == 2 && rows_per_tile % bm == 0) t = {bm, bn};
     }
     if (t.bm <= 0 || t.bm == 192) t = {256, 256};
-    return NormRelayResident(t.bm, t.bn, M, N, rows_per_tile, 0);
+    return NormRelayResident(dtype, t.bm, t.bn, M, N, K, rows_per_tile, 0);
 }
 
 void GemmStreamKNeeds(int M, int N, int K, size_t *ws_bytes, int *counters)

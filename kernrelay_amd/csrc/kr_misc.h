@@ -14,6 +14,8 @@ void RopeLaunch(int dtype, void *x, int64_t ld, int S, int heads, int D, const v
                 const void *sin_t, hipStream_t stream);
 void TransposeLaunch(const void *src, void *dst, int R, int C, hipStream_t stream);
 void FillLaunch(int32_t *p, int64_t n, int32_t v, hipStream_t stream);
+// n bf16 values of about N(0, std^2), a function of (seed, index) only.
+void RandBf16Launch(void *p, int64_t n, uint32_t seed, float std, hipStream_t stream);
 
 // Causal GQA attention, BSND layout: q [S, HQ, D], k/v [S, HKV, D],
 // out [S, HQ, D], each with its own row stride (elements; 0 = packed);

@@ -94,7 +94,46 @@ __global__ void __launch_bounds__(256) FillKernel(int32_t *p, int64_t n, int32_t
         p[i] = v;
 }
 
+// n bf16 values of about N(0, std^2) from a counter hash (Irwin-Hall sum of
+// four uniforms, scaled to unit variance): stand-in activations with the
+// bit activity of real ones.
+__device__ __forceinline__ uint32_t Hash32(uint32_t x)
+{
+    x ^= x >> 16;
+    x *= 0x7feb352du;
+    x ^= x >> 15;
+    x *= 0x846ca68bu;
+    x ^= x >> 16;
+    return x;
+}
+
+__global__ void __launch_bounds__(256) RandBf16Kernel(uint16_t *p, int64_t n, uint32_t seed, float std)
+{
+    for (int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; i < n;
+         i += int64_t(gridDim.x) * blockDim.x) {
+        uint32_t h = Hash32(uint32_t(i) ^ Hash32(seed ^ uint32_t(i >> 32)));
+        float s = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            h = Hash32(h + 0x9e3779b9u);
+            s += float(h >> 8) * (1.0f / 16777216.0f);
+        }
+        const float v = (s - 2.0f) * 1.7320508f * std;
+        uint32_t u = __float_as_uint(v);
+        u += 0x7fffu + ((u >> 16) & 1u);
+        p[i] = uint16_t(u >> 16);
+    }
+}
+
 }  // namespace
+
+void RandBf16Launch(void *p, int64_t n, uint32_t seed, float std, hipStream_t stream)
+{
+    if (n <= 0) return;
+    const int grid = int(std::min<int64_t>((n + 255) / 256, 8192));
+    hipLaunchKernelGGL(RandBf16Kernel, dim3(grid), dim3(256), 0, stream, static_cast<uint16_t *>(p), n, seed, std);
+    Check(hipGetLastError(), "rand fill launch");
+}
 
 void EmbedLaunch(const void *table, const int64_t *ids, void *out, int rows, int cols, int64_t vocab,
                  hipStream_t stream)

@@ -720,7 +720,17 @@ private:
             bool read = false;
             for (const auto &n : doc_.nodes)
                 if (std::find(n.preds.begin(), n.preds.end(), C.id) != n.preds.end()) read = true;
+            // a task that waits on C would wait on a release no launch makes
+            for (const auto &lane : doc_.lanes)
+                for (const auto &t : lane.tasks)
+                    for (const auto &w : t.waits)
+                        if (w.first == C.id) read = true;
             if (read) continue;
+            // what GemmLaunch asks of the unary output: 16-byte rows (the
+            // buffer itself is 256-byte aligned); otherwise the consumer
+            // keeps its own launch
+            if (C.out_dtype != kBF16 && C.out_dtype != kF16 && C.out_dtype != kF32) continue;
+            if ((C.cols * int64_t(DTypeBytes(C.out_dtype))) % 16 != 0) continue;
             const auto it = launch_of.find({P.id, 0});
             if (it == launch_of.end()) continue;
             Launch &PL = launches_[it->second];

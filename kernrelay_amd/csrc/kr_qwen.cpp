@@ -42,6 +42,7 @@
 
 #include <cmath>
 #include <cstdio>
+#include <cstring>
 #include <fstream>
 #include <functional>
 #include <map>
@@ -67,6 +68,9 @@ struct Mode {
     bool fused = false;    // fused Add+RMSNorm
     int tiles = 1;         // relay row tiles
     bool split = false;    // tile-released consumers with in-kernel waits
+    // relay_split flag edges (o -> Add+RMSNorm, down -> Add+RMSNorm); by
+    // default every edge whose relay tiles fit the device
+    bool edge_o = true, edge_down = true;
 };
 
 Mode ParseMode(const std::string &m)
@@ -90,8 +94,27 @@ Mode ParseMode(const std::string &m)
         md.dual = md.flags = md.fused = md.graph = md.split = true;
         md.tiles = 4;
         if (m.size() > 11) {
+            // relay_split:<k>[:<edges>], edges = o+down | o | down | none
             if (m[11] != ':') throw std::runtime_error("unknown mode " + m);
-            md.tiles = std::atoi(m.c_str() + 12);
+            const std::string rest = m.substr(12);
+            const size_t colon = rest.find(':');
+            const std::string ks = rest.substr(0, colon);
+            if (ks.empty() || ks.find_first_not_of("0123456789") != std::string::npos)
+                throw std::runtime_error("relay_split: tile count must be a number in 1..8");
+            md.tiles = std::atoi(ks.c_str());
+            if (colon != std::string::npos) {
+                const std::string edges = rest.substr(colon + 1);
+                if (edges == "o+down" || edges == "down+o") {
+                } else if (edges == "o") {
+                    md.edge_down = false;
+                } else if (edges == "down") {
+                    md.edge_o = false;
+                } else if (edges == "none") {
+                    md.edge_o = md.edge_down = false;
+                } else {
+                    throw std::runtime_error("relay_split: edges must be o+down, o, down or none");
+                }
+            }
         } else if (const char *e = std::getenv("KR_RELAY_TILES")) {
             md.tiles = std::atoi(e);
         }
@@ -129,9 +152,9 @@ public:
             if (g.first) (void)hipGraphDestroy(g.first);
         }
         for (hipEvent_t e : events_) (void)hipEventDestroy(e);
-        for (auto &pr : kev_) {
-            (void)hipEventDestroy(pr.first);
-            (void)hipEventDestroy(pr.second);
+        for (auto &t : kev_) {
+            (void)hipEventDestroy(t.a);
+            (void)hipEventDestroy(t.b);
         }
         if (t0_) (void)hipEventDestroy(t0_);
         if (tp_) (void)hipEventDestroy(tp_);
@@ -204,13 +227,14 @@ public:
             Check(hipDeviceSynchronize(), "pre timing sync");
             for (auto &it : prog_) it.fn(Stream(it.stream));
             Check(hipDeviceSynchronize(), "timing sync");
-            double sum = 0.0;
-            for (auto &pr : kev_) {
+            op_us_.clear();
+            op_n_.clear();
+            for (auto &t : kev_) {
                 float ms = 0.f;
-                Check(hipEventElapsedTime(&ms, pr.first, pr.second), "elapsed");
-                sum += 1000.0 * ms;
+                Check(hipEventElapsedTime(&ms, t.a, t.b), "elapsed");
+                op_us_[t.op] += 1000.0 * ms;
+                op_n_[t.op] += 1;
             }
-            gu_avg_us_ = sum / double(kev_.size());
         }
     }
 
@@ -304,9 +328,19 @@ public:
         std::snprintf(buf, sizeof buf, "%016llx", static_cast<unsigned long long>(fnv_));
         r.Set("logits_fnv64", Value::MakeString(buf));
         if (!kev_.empty()) {
-            // average gate/up GEMM duration in the eager timing pass
-            r.Set("gate_up_avg_us", Value::MakeNumber(gu_avg_us_));
-            r.Set("gate_up_launches", Value::MakeNumber(double(kev_.size())));
+            // average duration per labelled op in the eager timing pass
+            Value avg = Value::MakeObject(), n = Value::MakeObject();
+            for (const auto &kv : op_us_) {
+                const int c = op_n_.at(kv.first);
+                avg.Set(kv.first, Value::MakeNumber(kv.second / c));
+                n.Set(kv.first, Value::MakeNumber(c));
+            }
+            r.Set("op_avg_us", avg);
+            r.Set("op_launches", n);
+            if (op_n_.count("gate_up")) {
+                r.Set("gate_up_avg_us", Value::MakeNumber(op_us_.at("gate_up") / op_n_.at("gate_up")));
+                r.Set("gate_up_launches", Value::MakeNumber(op_n_.at("gate_up")));
+            }
         }
         r.Set("last_top2_margin", Value::MakeNumber(margin_));
         r.Set("consumer_cus", Value::MakeNumber(streams_.cons_cus));
@@ -733,18 +767,22 @@ private:
     }
 
     // ---------------------------------------------------------- relay split
-    // Bracket the ops emitted by `body` on stream s with timing events.
+    // Bracket the ops emitted by `body` on stream s with timing events,
+    // labelled `op` (KR_TIME_OPS=1: every labelled op; KR_TIME_GATE_UP=1:
+    // the gate/up GEMMs only).
     template <class F>
-    void Timed(int s, F body)
+    void Timed(int s, const char *op, F body)
     {
-        if (EnvInt("KR_TIME_GATE_UP", 0) == 0) {
+        const bool all = EnvInt("KR_TIME_OPS", 0) != 0;
+        const bool gu = EnvInt("KR_TIME_GATE_UP", 0) != 0 && std::strcmp(op, "gate_up") == 0;
+        if (!all && !gu) {
             body();
             return;
         }
         hipEvent_t a = nullptr, b = nullptr;
         Check(hipEventCreate(&a), "event");
         Check(hipEventCreate(&b), "event");
-        kev_.push_back({a, b});
+        kev_.push_back({op, a, b});
         Emit(s, [a](hipStream_t st) { Check(hipEventRecord(a, st), "record"); });
         prog_.back().timing = true;
         body();
@@ -771,7 +809,7 @@ private:
             gd.rope_d = D_;
             gd.rope_pos0 = 0;
         }
-        Emit(P, [gd](hipStream_t st) { GemmLaunch(gd, st); });
+        Timed(P, "qkv", [&] { Emit(P, [gd](hipStream_t st) { GemmLaunch(gd, st); }); });
         uint16_t *q = qkv, *kk = qkv + size_t(HQ_) * D_, *v = qkv + size_t(HQ_ + HKV_) * D_;
         int64_t ldq = ld, ldk = ld;
         if (qk_norm_) {
@@ -793,9 +831,11 @@ private:
         uint16_t *attn = attn_.as<uint16_t>();
         const float scale = float(1.0 / std::sqrt(double(D_)));
         const AttnSplit sp = attn_split_;
-        Emit(P, [=](hipStream_t st) {
-            AttnLaunch(kBF16, q, ldq, kk, ldk, v, ld, attn, int64_t(HQ) * D, S, HQ, HKV, D, scale, st,
-                       sp.ws != nullptr ? &sp : nullptr);
+        Timed(P, "attention", [&] {
+            Emit(P, [=](hipStream_t st) {
+                AttnLaunch(kBF16, q, ldq, kk, ldk, v, ld, attn, int64_t(HQ) * D, S, HQ, HKV, D, scale, st,
+                           sp.ws != nullptr ? &sp : nullptr);
+            });
         });
     }
 
@@ -847,8 +887,8 @@ private:
         // relay tile's producer workgroups fit the device at once
         // (KR_SPLIT_NORM=0: Add+RMSNorm as a kernel after the GEMM)
         const bool norm_env = EnvInt("KR_SPLIT_NORM", 1) != 0;
-        const bool o_relay = norm_env && GemmNormRelayFits(S, H_, HQ_ * D_, T, skws_bytes_ > 0);
-        const bool d_relay = norm_env && GemmNormRelayFits(S, H_, I_, T, skws_bytes_ > 0);
+        const bool o_relay = norm_env && mode_.edge_o && GemmNormRelayFits(S, H_, HQ_ * D_, T, skws_bytes_ > 0);
+        const bool d_relay = norm_env && mode_.edge_down && GemmNormRelayFits(S, H_, I_, T, skws_bytes_ > 0);
         const int o_edge = o_relay ? NewEdge(k * L_) : 0;
         const int d_edge = d_relay ? NewEdge(k * L_) : 0;
         for (int b = 0; b < (o_relay ? k * L_ : 0); ++b) consumed_.push_back(o_edge + b);
@@ -872,14 +912,18 @@ private:
             const Layer &w = layers_[l];
             EmitAttention(P, l, RelayWait{});
             if (o_relay) {
-                GemmNormRelay(P, attn_.get(), int64_t(HQ_) * D_, w.o, HQ_ * D_, o_.get(), Pub(o_edge + l * k, T), hcur,
-                              w.ln2, x, hnxt);
+                Timed(P, "o", [&] {
+                    GemmNormRelay(P, attn_.get(), int64_t(HQ_) * D_, w.o, HQ_ * D_, o_.get(), Pub(o_edge + l * k, T),
+                                  hcur, w.ln2, x, hnxt);
+                });
             } else {
-                Gemm(P, attn_.get(), int64_t(HQ_) * D_, w.o, H_, HQ_ * D_, o_.get(), H_, nullptr, S, RelayPub{});
-                AddRmsNorm(P, hcur, o_.get(), w.ln2, x, hnxt, RelayWait{}, 0, RelayPub{}, 0);
+                Timed(P, "o", [&] {
+                    Gemm(P, attn_.get(), int64_t(HQ_) * D_, w.o, H_, HQ_ * D_, o_.get(), H_, nullptr, S, RelayPub{});
+                });
+                Timed(P, "add_rmsnorm", [&] { AddRmsNorm(P, hcur, o_.get(), w.ln2, x, hnxt, RelayWait{}, 0, RelayPub{}, 0); });
             }
             if (swiglu_kernel) {
-                Timed(P, [&] {
+                Timed(P, "gate_up", [&] {
                     Gemm(P, x, H_, w.gu, 2 * I_, H_, gu_.get(), 2 * int64_t(I_), nullptr, S, RelayPub{}, RelayWait{},
                          false);
                 });
@@ -906,7 +950,7 @@ private:
                 d.K = H_;
                 d.epi_act = act_.get();
                 d.ld_act = I_;
-                Timed(P, [&] { Emit(P, [d](hipStream_t st) { GemmLaunch(d, st); }); });
+                Timed(P, "gate_up", [&] { Emit(P, [d](hipStream_t st) { GemmLaunch(d, st); }); });
             } else {
                 // gate/up, its k released tiles consumed by the appended SwiGLU
                 GemmDesc d;
@@ -926,7 +970,7 @@ private:
                 d.tail_tiles = tail_tiles;
                 d.order_rows = order_rows;
                 for (int t = 0; t < tail_tiles; ++t) consumed_.push_back(gu_act + l * k + t);
-                Timed(P, [&] {
+                Timed(P, "gate_up", [&] {
                     if (tail_tiles > 0) {
                         Emit(P, [d](hipStream_t st) { GemmLaunch(d, st); });
                     } else {
@@ -949,14 +993,18 @@ private:
             void *y_next = last ? xf_.get() : x_.get();
             void *h_next = last ? hf_.get() : static_cast<void *>(hcur);
             if (d_relay) {
-                GemmNormRelay(P, act_.get(), I_, w.down, I_, down_.get(), Pub(d_edge + l * k, T), hnxt, g_next, y_next,
-                              h_next);
+                Timed(P, "down", [&] {
+                    GemmNormRelay(P, act_.get(), I_, w.down, I_, down_.get(), Pub(d_edge + l * k, T), hnxt, g_next,
+                                  y_next, h_next);
+                });
             } else {
-                Gemm(P, act_.get(), I_, w.down, H_, I_, down_.get(), H_, nullptr, S, RelayPub{});
-                AddRmsNorm(P, hnxt, down_.get(), g_next, y_next, h_next, RelayWait{}, 0, RelayPub{}, 0);
+                Timed(P, "down", [&] { Gemm(P, act_.get(), I_, w.down, H_, I_, down_.get(), H_, nullptr, S, RelayPub{}); });
+                Timed(P, "add_rmsnorm", [&] {
+                    AddRmsNorm(P, hnxt, down_.get(), g_next, y_next, h_next, RelayWait{}, 0, RelayPub{}, 0);
+                });
             }
         }
-        Gemm(P, xf_.get(), H_, lm_, V_, H_, logits_.get(), V_, nullptr, S, RelayPub{});
+        Timed(P, "lm_head", [&] { Gemm(P, xf_.get(), H_, lm_, V_, H_, logits_.get(), V_, nullptr, S, RelayPub{}); });
     }
 
     // A [S, H] projection (o or down) into C whose k released row tiles are
@@ -1032,15 +1080,17 @@ private:
             if (mode_.dual && l > 0) WaitBefore(P, le[l - 1].exit, k);
             EmitAttention(P, l, RelayWait{});
             // o_proj -> Add+RMSNorm(post_attention_layernorm)
-            Gemm(P, attn_.get(), int64_t(HQ_) * D_, w.o, H_, HQ_ * D_, o_.get(), H_, nullptr, S,
-                 release(le[l].o_ln2));
+            Timed(P, "o", [&] {
+                Gemm(P, attn_.get(), int64_t(HQ_) * D_, w.o, H_, HQ_ * D_, o_.get(), H_, nullptr, S,
+                     release(le[l].o_ln2));
+            });
             after(P, le[l].o_ln2);
             AddRmsNorm(C, hcur, o_.get(), w.ln2, x, hnxt, consumer_wait(le[l].o_ln2), ctile, release(le[l].ln2_gu),
                        cgrid);
             after(C, le[l].ln2_gu);
             // gate/up -> SwiGLU
             WaitBefore(P, le[l].ln2_gu, k);
-            Timed(P, [&] {
+            Timed(P, "gate_up", [&] {
                 Gemm(P, x, H_, w.gu, 2 * I_, H_, gu_.get(), 2 * int64_t(I_), nullptr, S, release(le[l].gu_act),
                      RelayWait{}, false);
             });
@@ -1061,7 +1111,7 @@ private:
             }
             // down -> Add+RMSNorm(next input_layernorm | final norm)
             WaitBefore(P, le[l].act_down, k);
-            Gemm(P, act_.get(), I_, w.down, H_, I_, down_.get(), H_, nullptr, S, release(le[l].down_ln));
+            Timed(P, "down", [&] { Gemm(P, act_.get(), I_, w.down, H_, I_, down_.get(), H_, nullptr, S, release(le[l].down_ln)); });
             after(P, le[l].down_ln);
             const RelayWait wd = consumer_wait(le[l].down_ln);
             if (l + 1 < L_) {
@@ -1073,7 +1123,7 @@ private:
             after(C, le[l].exit);
         }
         if (mode_.dual) WaitBefore(P, le[L_ - 1].exit, k);
-        Gemm(P, xf_.get(), H_, lm_, V_, H_, logits_.get(), V_, nullptr, S, RelayPub{});
+        Timed(P, "lm_head", [&] { Gemm(P, xf_.get(), H_, lm_, V_, H_, logits_.get(), V_, nullptr, S, RelayPub{}); });
     }
 
     void Capture()
@@ -1121,6 +1171,7 @@ private:
     DevBuf ctrl_;
     DevBuf skws_, skcnt_;  // stream-K partials and tile counters
     DevBuf attn_ws_, attn_cnt_;  // attention split partials and tickets
+    std::vector<DevBuf> prof_ctrl_;  // relay control blocks of profiled relay ops
     AttnSplit attn_split_{};
     size_t skws_bytes_ = 0;
     int skcnt_len_ = 0;
@@ -1130,10 +1181,15 @@ private:
     std::vector<hipEvent_t> events_;
     uint32_t max_spins_ = kDefaultMaxSpins;
     hipEvent_t t0_ = nullptr, tp_ = nullptr, tc_ = nullptr;
-    // KR_TIME_GATE_UP=1: timing events around every gate/up GEMM, recorded in
-    // one eager pass of the program after the timed iterations
-    std::vector<std::pair<hipEvent_t, hipEvent_t>> kev_;
-    double gu_avg_us_ = 0.0;
+    // KR_TIME_OPS=1 / KR_TIME_GATE_UP=1: timing events around labelled ops,
+    // recorded in one eager pass of the program after the timed iterations
+    struct OpTiming {
+        std::string op;
+        hipEvent_t a, b;
+    };
+    std::vector<OpTiming> kev_;
+    std::map<std::string, double> op_us_;
+    std::map<std::string, int> op_n_;
     std::vector<double> samples_, host_samples_, dev_samples_;
     int argmax_ = -1, ref_argmax_ = -1, flag_edges_ = 0, flag_timeouts_ = 0;
     double maxdiff_ = -1.0, absmean_ = 0.0, margin_ = 0.0, load_ms_ = 0.0;
@@ -1147,6 +1203,16 @@ std::string Model::ProfileMany(const std::string &spec_path)
     const Value spec = json::ParseFile(spec_path);
     const int rows = seq_;
     hipStream_t st = streams_.prod;
+    // every activation buffer holds seeded N(0,1) bf16 values before any op
+    // is timed: a GEMM fed never-written (zero) activations draws less power
+    // and the card holds a higher clock (MI355X, 2048x3584x18944: 181 us on
+    // zeros against 250 us on a prefill's activations)
+    {
+        uint32_t seed = 1;
+        for (DevBuf *b : {&h_[0], &h_[1], &x_, &qkv_, &attn_, &o_, &gu_, &act_, &down_, &hf_, &xf_})
+            if (b->bytes() >= 2) RandBf16Launch(b->get(), int64_t(b->bytes() / 2), seed++, 1.0f, st);
+        Check(hipStreamSynchronize(st), "profile input fill");
+    }
     std::vector<std::string> cases;
     const Layer &w = layers_.at(0);
     const int64_t ld = ldqkv_;
@@ -1161,7 +1227,33 @@ std::string Model::ProfileMany(const std::string &spec_path)
             return static_cast<void *>(b.as<uint16_t>() + size_t(i) * per * cols);
         };
         try {
-            if (op.rfind("matmul_", 0) == 0) {
+            if (op == "matmul_o_add_rmsnorm_relay" || op == "matmul_down_add_rmsnorm_relay") {
+                // the relay split's o / down edge: one GEMM launch releasing
+                // k row tiles, each consumed at once by Add+RMSNorm in the
+                // GEMM's own workgroups (relay_split's GemmNormRelay)
+                const bool is_o = op == "matmul_o_add_rmsnorm_relay";
+                const int K = is_o ? HQ_ * D_ : I_;
+                if (per % 64 != 0 || !GemmNormRelayFits(rows, H_, K, per, skws_bytes_ > 0)) continue;
+                prof_ctrl_.emplace_back(size_t(k) * kWords * 4);
+                DevBuf &ctrl = prof_ctrl_.back();
+                Check(hipMemset(ctrl.get(), 0, ctrl.bytes()), "zero profile ctrl");
+                RelayPub pub{};
+                pub.ctrl = ctrl.as<int32_t>();
+                pub.flag0 = 0;
+                pub.rows_per_tile = per;
+                GemmDesc d = MakeGemm(is_o ? attn_.get() : act_.get(), K, is_o ? w.o : w.down, H_, K,
+                                      is_o ? o_.get() : down_.get(), H_, nullptr, rows, pub, RelayWait{});
+                d.norm_res = h_[0].get();
+                d.norm_gamma = w.ln2;
+                d.norm_y = x_.get();
+                d.norm_sum = h_[1].get();
+                d.norm_rstd = rstd_.as<float>();
+                d.norm_eps = float(eps_);
+                d.norm_max_spins = kDefaultMaxSpins;
+                shape = "matmul_add_rmsnorm_relay|" + std::to_string(rows) + "x" + std::to_string(K) + "x" +
+                        std::to_string(H_);
+                calls.push_back([d](hipStream_t s) { GemmLaunch(d, s); });
+            } else if (op.rfind("matmul_", 0) == 0) {
                 const void *A = x_.get();
                 int64_t K = H_, N = H_, lda = H_;
                 const uint16_t *Bt = nullptr;

@@ -7,7 +7,8 @@
   relay split at k = 1, 2, 4, 8 (schedules from kernrelay_amd.schedule, as
   the reference's E3/E4 variants, python/kernrelay/e34.py:16-22);
 * the reference's own relay cases (fp16 32768x1024x2048 GEMM -> GELU,
-  softmax, cast, {GELU, softmax}) at its k, next to its published times;
+  softmax, cast, {GELU, softmax}; the reverse edge LayerNorm 32768x2048 ->
+  GEMM 2048x2048) at its k, next to its published times;
   for an elementwise consumer also the in-register relay (the same split
   schedule with the consumer computed in the GEMM's epilogue,
   KR_PLAN_EPILOGUE=1);
@@ -122,20 +123,24 @@ E34_REFERENCE = {
     "mm_softmax_k4": (["softmax"], 4, 1133.0, 1132.3, 888.4),
     "mm_cast_k4": (["cast"], 4, 1018.6, 966.3, 944.2),
     "mm_fanout_gelu_softmax_k4": (["gelu", "softmax"], 4, 1406.1, 1424.5, 1318.3),
+    # the reverse edge: LayerNorm [32768, 2048] releasing row tiles to the
+    # GEMM (K = N = 2048) that reads them as A (RESULTS.md:73)
+    "e3_ln_mm_k4": (None, 4, 1890.3, 1885.5, 1456.8),
 }
 
 
 def reference_e34(tmp, iters=20, warmup=3):
     """The reference's own relay cases at its shapes and dtype (fp16 GEMM
-    32768x1024x2048 -> consumers, DetValue inputs, one rank): serial, B0 and
-    the split at the reference's k, with the reference's published times
+    32768x1024x2048 -> consumers, and the reverse edge LayerNorm
+    32768x2048 -> GEMM K = N = 2048; DetValue inputs, one rank): serial, B0
+    and the split at the reference's k, with the reference's published times
     beside ours."""
     out = {}
     for case, (consumers, k, r_serial, r_b0, r_split) in E34_REFERENCE.items():
         dag = workloads.e34_dag(case, consumers)
         v = workloads.variants(dag, k)
         rs = {name: _plan(v[name], tmp, "%s_%s" % (case, name), iters, warmup) for name in ("serial", "b0", "split")}
-        if len(consumers) == 1 and consumers[0] in ("gelu", "silu", "cast"):
+        if consumers is not None and len(consumers) == 1 and consumers[0] in ("gelu", "silu", "cast"):
             # the same split schedule with the consumer in the GEMM's epilogue
             rs["register_relay"] = _plan(v["split"], tmp, "%s_epi" % case, iters, warmup, env={"KR_PLAN_EPILOGUE": "1"})
         ours = {name: round(rs[name]["device_best_us"], 2) for name in rs}

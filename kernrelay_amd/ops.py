@@ -164,6 +164,15 @@ def gemm_add_rmsnorm(A, Bt, C, res, gamma, y, pub, sum_out=None, rstd=None, eps=
     M, K = A.shape
     N = Bt.shape[0]
     assert Bt.shape[1] == K and C.shape == (M, N) and res.shape == (M, N) and y.shape == (M, N)
+    # the C entry takes C, res, y and sum_out as packed [M, N] rows and rstd
+    # as [M]: a strided view would be read or written with row stride N
+    for name, t in (("C", C), ("res", res), ("y", y), ("sum_out", sum_out), ("rstd", rstd), ("gamma", gamma)):
+        if t is not None and not t.is_contiguous():
+            raise ValueError("gemm_add_rmsnorm: %s must be contiguous" % name)
+    if sum_out is not None and sum_out.shape != (M, N):
+        raise ValueError("gemm_add_rmsnorm: sum_out must be [M, N]")
+    if rstd is not None and rstd.numel() != M:
+        raise ValueError("gemm_add_rmsnorm: rstd must hold M values")
     _check(_lib().kr_op_gemm_add_rmsnorm(_dt(A), _ptr(A), A.stride(0), _ptr(Bt), Bt.stride(0), _ptr(C), M, N, K,
                                          _ptr(res), _ptr(gamma), _ptr(y), _ptr(sum_out), _ptr(rstd), ctypes.c_float(eps),
                                          ctypes.byref(pub), ctypes.c_uint32(max_spins), _ptr(ws),

@@ -862,6 +862,48 @@ PROFILE_OPS = ("embedding", "rmsnorm", "add", "add_rmsnorm", "rope",
                "matmul_lm")
 
 
+# the relay split's flag edges, each timed as one relayed launch (the GEMM
+# releasing k row tiles, its own workgroups running Add+RMSNorm on each) next
+# to the same work unrelayed (the GEMM, then the Add+RMSNorm kernel)
+RELAY_EDGES = {"o": ("matmul_o_add_rmsnorm_relay", "matmul_o"),
+               "down": ("matmul_down_add_rmsnorm_relay", "matmul_down")}
+RELAY_PROFILE_OPS = tuple(v[0] for v in RELAY_EDGES.values()) + ("matmul_gate_up", "swiglu")
+
+
+def relay_edges(table, k, launch_us=0.0):
+    """The relay split's flag edges that pay at k tiles on a measured table.
+
+    An edge is taken only where its relayed launch beats the unrelayed pair
+    (the GEMM, the Add+RMSNorm kernel and the extra kernel's launch in a
+    replayed graph), as the reference's planner keeps a split only where it
+    lowers the makespan (planner2.py:581-671). Returns (edges, detail):
+    edges in RELAY_EDGES order, detail = {edge: {relay_us, unrelayed_us,
+    gain_us}} for every edge the table prices."""
+    def col(v, kk):
+        return None if v is None else v.get(kk, v.get(str(kk)))
+
+    edges, detail = [], {}
+    norm = col(table.get("add_rmsnorm"), 1)
+    for name, (relay_op, gemm_op) in RELAY_EDGES.items():
+        r, g = col(table.get(relay_op), k), col(table.get(gemm_op), 1)
+        if r is None or g is None or norm is None:
+            continue
+        unrelayed = float(g) + float(norm) + float(launch_us)
+        gain = unrelayed - float(r)
+        detail[name] = {"relay_us": round(float(r), 3), "unrelayed_us": round(unrelayed, 3),
+                        "gain_us": round(gain, 3)}
+        if gain > 0:
+            edges.append(name)
+    return edges, detail
+
+
+def relay_mode(table, k, launch_us=0.0):
+    """kr_qwen_run mode string of the relay split with the edges that pay
+    (relay_split:<k>:<edges>; "none" when no edge does)."""
+    edges, _ = relay_edges(table, k, launch_us)
+    return "relay_split:%d:%s" % (k, "+".join(edges) if edges else "none")
+
+
 def profile_op(node):
     """``kr_qwen_profile_many`` op name that times a DAG node
     (optimize.py:193-207)."""

@@ -2,7 +2,11 @@
 
 * ``profile``          — ``kr_qwen_profile_many`` over the reference's op list
                          at k = 1, 2, 4, 8 row slices (scripts/profile_model.py:
-                         13-34): op -> {k: best_us}.
+                         13-34): op -> {k: best_us}; plus the relay split's
+                         own launches (the o / down GEMM releasing k row
+                         tiles to Add+RMSNorm in its workgroups, the fused
+                         gate/up GEMM, SwiGLU), which price its flag edges
+                         (planner.relay_edges).
 * ``measure_constants`` — the cost file's scalars (configs/planner2_costs.json
                          keys): ``launch_us`` (one more kernel in a replayed
                          graph), ``event_us`` (an event record on one stream
@@ -225,8 +229,9 @@ def main(argv=None):
         cfg = json.loads((mdir / "manifest.json").read_text())["config"]
         ks = [int(k) for k in args.ks.split(",")]
         t0 = time.time()
-        log("kr_qwen_profile_many %d ops x k=%s" % (len(planner.PROFILE_OPS), ks))
-        prof = profile(mdir, args.seq, args.device, ks)
+        ops = planner.PROFILE_OPS + planner.RELAY_PROFILE_OPS
+        log("kr_qwen_profile_many %d ops x k=%s" % (len(ops), ks))
+        prof = profile(mdir, args.seq, args.device, ks, ops=ops)
         log("profile done in %.1f s" % (time.time() - t0))
         Path(args.out).write_text(json.dumps(prof, indent=1))
         if args.costs_out:

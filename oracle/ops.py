@@ -134,8 +134,13 @@ def rope(x, cos, sin, dt=torch.bfloat16):
     return rnd(torch.cat([o1, o2], dim=-1), dt)
 
 
-def attention(q, k, v, scale=None, dt=torch.bfloat16):
-    """Causal GQA attention. q [S, HQ, D], k/v [S, HKV, D] -> [S, HQ, D] (fp32 softmax)."""
+def attention(q, k, v, scale=None, dt=torch.bfloat16, p_dt=None):
+    """Causal GQA attention. q [S, HQ, D], k/v [S, HKV, D] -> [S, HQ, D] (fp32 softmax).
+
+    p_dt (e.g. torch.bfloat16): the products P.V take P rounded to p_dt, as
+    a 16-bit matrix unit does: P = exp(s - rowmax) in fp32, rounded to p_dt
+    before the P.V product (fp32 accumulation), then divided by the fp32 sum
+    of the unrounded P. None: P stays fp32 (the reference's softmax)."""
     S, HQ, D = q.shape
     HKV = k.shape[1]
     scale = scale if scale is not None else 1.0 / math.sqrt(D)
@@ -146,8 +151,12 @@ def attention(q, k, v, scale=None, dt=torch.bfloat16):
     scores = torch.matmul(qh, kh.transpose(1, 2).contiguous()) * scale
     mask = torch.ones(S, S, dtype=torch.bool).triu(1)
     scores = scores.masked_fill(mask, float("-inf"))
-    p = torch.softmax(scores, dim=-1)
-    return rnd(torch.matmul(p, vh).permute(1, 0, 2), dt)
+    if p_dt is None:
+        p = torch.softmax(scores, dim=-1)
+        return rnd(torch.matmul(p, vh).permute(1, 0, 2), dt)
+    e = torch.exp(scores - scores.amax(dim=-1, keepdim=True))
+    num = torch.matmul(rnd(e, p_dt), vh)
+    return rnd((num / e.sum(dim=-1, keepdim=True)).permute(1, 0, 2), dt)
 
 
 def embedding(table, ids):

@@ -64,9 +64,10 @@ class ModelDir:
         return cos, sin
 
 
-def layer_forward(m, l, h, x, cos, sin):
+def layer_forward(m, l, h, x, cos, sin, p_dt=None):
     """One decoder layer. h = residual stream (bf16 values), x = normed input.
-    Returns (h_next, x_next_unnormed_sum) where the caller applies the next norm."""
+    Returns (h_next, x_next_unnormed_sum) where the caller applies the next norm.
+    p_dt: attention's P rounded to this type before P.V (ops.attention)."""
     S = x.shape[0]
     p = "L%02d." % l
     HQ, HKV, D = m.HQ, m.HKV, m.D
@@ -81,7 +82,7 @@ def layer_forward(m, l, h, x, cos, sin):
         k, _ = ops.rmsnorm(k, m.tensor(p + "k_norm.weight"), m.eps)
     q = ops.rope(q, cos, sin)
     k = ops.rope(k, cos, sin)
-    a = ops.attention(q, k, v).reshape(S, HQ * D)
+    a = ops.attention(q, k, v, p_dt=p_dt).reshape(S, HQ * D)
     o = ops.gemm(a, m.tensor(p + "o_proj.weight_t"))
     x2, h2, _ = ops.add_rmsnorm(h, o, m.tensor(p + "post_attention_layernorm.weight"), m.eps)
     g = ops.gemm(x2, m.tensor(p + "gate_proj.weight_t"))
@@ -91,9 +92,15 @@ def layer_forward(m, l, h, x, cos, sin):
     return h2, d
 
 
-def prefill(model_dir, layers=None, threads=None):
+def prefill(model_dir, layers=None, threads=None, lm_all_rows=False, p_dt=None):
     """Run the prefill; returns dict(last_logits=fp32 [V] of bf16 values,
-    argmax, margin). `layers` truncates the stack (tests of the CPU cost)."""
+    argmax, margin). `layers` truncates the stack (tests of the CPU cost).
+    lm_all_rows: compute the lm_head over every row, as the reference's
+    prefill does (qwen_main.cpp:920, :989), instead of the last row only
+    (the work of a timed baseline; the last row then differs from the
+    one-row product only by fp32 summation order). p_dt: attention's P
+    rounded to this type before P.V, as a 16-bit matrix unit computes it
+    (ops.attention)."""
     if threads:
         torch.set_num_threads(threads)
     m = model_dir if isinstance(model_dir, ModelDir) else ModelDir(model_dir)
@@ -105,10 +112,10 @@ def prefill(model_dir, layers=None, threads=None):
         x, _ = ops.rmsnorm(h, m.tensor("L00.input_layernorm.weight"), m.eps)
         L = m.L if layers is None else layers
         for l in range(L):
-            h2, d = layer_forward(m, l, h, x, cos, sin)
+            h2, d = layer_forward(m, l, h, x, cos, sin, p_dt=p_dt)
             gname = ("L%02d.input_layernorm.weight" % (l + 1)) if l + 1 < L else "final_norm.weight"
             x, h, _ = ops.add_rmsnorm(h2, d, m.tensor(gname), m.eps)
-        logits = ops.gemm(x[-1:], m.tensor("lm_head.weight_t"))[0]
+        logits = ops.gemm(x if lm_all_rows else x[-1:], m.tensor("lm_head.weight_t"))[-1]
     top = torch.topk(logits, 2)
     return {"last_logits": logits, "argmax": int(top.indices[0]),
             "margin": float(top.values[0] - top.values[1])}

@@ -95,3 +95,24 @@ def test_unknown_op_and_mode_rejected(tmp_path):
     assert "RC 1" in proc.stdout and "not built" in proc.stderr
     proc = run_plan_subprocess(schedule.dump_schedule(sched, tmp_path / "ok.json"), mode="graph_bogus")
     assert "RC 1" in proc.stdout and "not built" in proc.stderr
+
+
+def test_gemm_add_rmsnorm_rejects_strided_views():
+    """The C entry takes C, res, y and sum as packed [M, N] rows: a strided
+    view is refused before anything reaches the library."""
+    import torch
+
+    from kernrelay_amd import ops
+
+    M, N, K = 64, 256, 64
+    A = torch.zeros(M, K, dtype=torch.bfloat16)
+    Bt = torch.zeros(N, K, dtype=torch.bfloat16)
+    wide = torch.zeros(M, N + 8, dtype=torch.bfloat16)
+    packed = torch.zeros(M, N, dtype=torch.bfloat16)
+    gamma = torch.ones(N, dtype=torch.bfloat16)
+    pub = ops.KrPub(None, 0, M, 0)
+    for bad in ("C", "res", "y", "sum_out"):
+        args = {"C": packed, "res": packed, "y": packed, "sum_out": packed}
+        args[bad] = wide[:, :N]
+        with pytest.raises(ValueError, match=bad):
+            ops.gemm_add_rmsnorm(A, Bt, args["C"], args["res"], gamma, args["y"], pub, sum_out=args["sum_out"])

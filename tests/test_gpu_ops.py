@@ -276,6 +276,29 @@ def test_attention(gpu, S, HQ, HKV, D):
     close(out, O.attention(q.float(), k.float(), v.float()))
 
 
+@pytest.mark.parametrize("S,HQ,HKV,D,dt", [(4096, 64, 8, 64, torch.bfloat16), (512, 6, 3, 128, torch.bfloat16),
+                                            (300, 6, 3, 64, torch.bfloat16), (1024, 8, 2, 128, torch.float16),
+                                            (4096, 64, 8, 64, torch.float16)])
+def test_attention_kernel_variants(gpu, S, HQ, HKV, D, dt):
+    """Kernel variants the model shapes leave out, against the oracle on the
+    first and last query-head groups: the 4-wave kernel at head size 64 (4096
+    x 64 heads: 4096 workgroups, more than one resident round), the plain
+    workgroup order where HKV neither divides nor is divided by the 8 XCDs
+    (HKV 3), and fp16 inputs and outputs (fp16 MFMA, P rounded to fp16)."""
+    announce("attention variant S=%d HQ=%d HKV=%d D=%d %s" % (S, HQ, HKV, D, dt))
+    q = rand((S, HQ, D), 1.0, 40, dt)
+    k = rand((S, HKV, D), 1.0, 41, dt)
+    v = rand((S, HKV, D), 1.0, 42, dt)
+    out = torch.empty(S, HQ, D, dtype=dt, device="cuda")
+    ops.attention(q.cuda(), k.cuda(), v.cuda(), out, S, HQ, HKV, D)
+    torch.cuda.synchronize()
+    rep = HQ // HKV
+    for g in sorted({0, HKV - 1}):
+        hs = slice(g * rep, (g + 1) * rep)
+        ref = O.attention(q[:, hs].float(), k[:, g:g + 1].float(), v[:, g:g + 1].float(), dt=dt)
+        close(out[:, hs], ref)
+
+
 @pytest.mark.parametrize("S,HQ,HKV,D", [(2048, 7, 1, 64), (1500, 3, 1, 128), (4096, 4, 2, 64), (1100, 2, 2, 64)])
 def test_attention_split(gpu, S, HQ, HKV, D):
     """Long causal rows split across workgroups (query blocks of more than 16
@@ -587,7 +610,7 @@ def _streamk_case(M, N, K, bias):
 @pytest.mark.parametrize("M,N,K,k,streamk", [(2048, 3584, 3584, 1, False), (2048, 3584, 3584, 4, False),
                                              (2048, 3584, 18944, 8, False), (2048, 896, 4864, 4, True),
                                              (2048, 896, 4864, 2, False), (256, 256, 512, 4, False),
-                                             (512, 4096, 1024, 2, False)])
+                                             (512, 4096, 1024, 2, False), (8192, 4096, 512, 4, False)])
 def test_gemm_add_rmsnorm_relay_bit_exact(gpu, M, N, K, k, streamk):
     """The row-tiled relay of a projection to its Add+RMSNorm consumer: the
     GEMM releases k row tiles and its own workgroups normalise each released
@@ -596,7 +619,10 @@ def test_gemm_add_rmsnorm_relay_bit_exact(gpu, M, N, K, k, streamk):
     Qwen2.5-0.5B down shape with its four-piece K split, 64-row tiles); every
     relay tile's block ends with published == consumed == runs and status 1
     over repeated runs without a host reset; y matches the oracle's
-    Add+RMSNorm of the stored product."""
+    Add+RMSNorm of the stored product. 8192x4096 with k=4 is a grid of two
+    rounds (512 workgroups of 256x256, 128 per relay tile) that runs in
+    relay-tile order: the later tiles' workgroups start only as the earlier
+    tiles' finish their Add+RMSNorm."""
     announce("gemm+add_rmsnorm relay %dx%dx%d k=%d streamk=%s" % (M, N, K, k, streamk))
     g = torch.Generator(device="cuda").manual_seed(60)
     A = torch.randn(M, K, device="cuda", generator=g).to(torch.bfloat16)

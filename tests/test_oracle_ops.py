@@ -137,6 +137,49 @@ def test_attention_brute_force_gqa_causal():
     assert torch.equal(O.attention(q, k2, v2)[:-1], O.attention(q, k, v)[:-1])
 
 
+def test_attention_rounded_p_brute_force():
+    """attention(p_dt=bf16) against a loop that rounds each unnormalised
+    weight exp(s_j - max) to bf16 before weighting v_j and divides by the sum
+    of the unrounded weights. Planted variants that round the normalised
+    softmax instead, or divide by the sum of the rounded weights, or skip the
+    rounding, each miss it by far more than the loop's own float error."""
+    torch.manual_seed(5)
+    S, HQ, HKV, D = 9, 4, 2, 16
+    q, k, v = bf(3 * torch.randn(S, HQ, D)), bf(3 * torch.randn(S, HKV, D)), bf(torch.randn(S, HKV, D))
+
+    def loop(variant):
+        out = torch.zeros(S, HQ, D, dtype=torch.float64)
+        for h in range(HQ):
+            kv = h // (HQ // HKV)
+            for i in range(S):
+                sc = [float(q[i, h].double() @ k[j, kv].double()) / math.sqrt(D) for j in range(i + 1)]
+                m = max(sc)
+                e = [math.exp(t - m) for t in sc]
+                z = sum(e)
+                er = [float(torch.tensor(t, dtype=torch.float32).to(torch.bfloat16)) for t in e]
+                if variant == "round_normalised":
+                    w = [float(torch.tensor(t / z).to(torch.bfloat16)) for t in e]
+                    z = 1.0
+                elif variant == "sum_rounded":
+                    w, z = er, sum(er)
+                elif variant == "unrounded":
+                    w = e
+                else:
+                    w = er
+                for j in range(i + 1):
+                    out[i, h] += w[j] * v[j, kv].double()
+                out[i, h] /= z
+        return out
+
+    got = O.attention(q, k, v, dt=torch.float32, p_dt=torch.bfloat16).double()
+    good = (got - loop("ok")).abs().max().item()
+    assert good < 2e-5, good
+    for bad in ("round_normalised", "sum_rounded", "unrounded"):
+        assert (got - loop(bad)).abs().max().item() > 20 * max(good, 1e-6), bad
+    # p_dt=None is the fp32 softmax
+    assert torch.equal(O.attention(q, k, v, p_dt=None), O.attention(q, k, v))
+
+
 def test_embedding():
     t = bf(torch.randn(50, 16))
     ids = torch.tensor([3, 0, 49, 3])

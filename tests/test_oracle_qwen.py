@@ -80,10 +80,10 @@ def test_oracle_matches_transformers_wide_init(dirs, hf_logits, preset):
 _ORIG = {n: getattr(O, n) for n in ("gemm", "rope", "add_rmsnorm", "attention", "swiglu", "rmsnorm")}
 
 
-def _gqa_tiled(q, k, v, scale=None, dt=torch.bfloat16):
+def _gqa_tiled(q, k, v, scale=None, dt=torch.bfloat16, p_dt=None):
     # query head h reads kv head h % HKV instead of h // (HQ / HKV)
     rep = q.shape[1] // k.shape[1]
-    return _ORIG["attention"](q, k.repeat(1, rep, 1), v.repeat(1, rep, 1), scale, dt)
+    return _ORIG["attention"](q, k.repeat(1, rep, 1), v.repeat(1, rep, 1), scale, dt, p_dt)
 
 
 MISTAKES = {
@@ -93,8 +93,8 @@ MISTAKES = {
     "rope sign flipped": dict(rope=lambda x, c, s, dt=torch.bfloat16: _ORIG["rope"](x, c, -s, dt)),
     "rope skipped": dict(rope=lambda x, c, s, dt=torch.bfloat16: x),
     "gqa heads tiled": dict(attention=_gqa_tiled),
-    "attention scale 1/D": dict(attention=lambda q, k, v, scale=None, dt=torch.bfloat16:
-                                _ORIG["attention"](q, k, v, 1.0 / q.shape[-1], dt)),
+    "attention scale 1/D": dict(attention=lambda q, k, v, scale=None, dt=torch.bfloat16, p_dt=None:
+                                _ORIG["attention"](q, k, v, 1.0 / q.shape[-1], dt, p_dt)),
     "gate and up swapped": dict(swiglu=lambda g, u, dt=torch.bfloat16: _ORIG["swiglu"](u, g, dt)),
     "norm gain dropped": dict(rmsnorm=lambda x, g, eps, dt=torch.bfloat16:
                               _ORIG["rmsnorm"](x, torch.ones_like(g), eps, dt)),

@@ -289,3 +289,21 @@ def test_shipped_mi355x_costs_cover_the_7b_dag():
     # serial lower bound: the aic queue alone
     aic = sum(costs.base(n) for n in dag["nodes"] if n["engine"] in ("aic", "aicore"))
     assert plan["base_makespan_us"] >= aic
+
+
+def test_relay_edges_taken_only_where_they_pay():
+    """An o / down flag edge is kept only where its one relayed launch beats
+    the GEMM, the Add+RMSNorm kernel and one more launch; the mode string
+    names the edges kept."""
+    table = {"matmul_o": {1: 55.0}, "matmul_down": {1: 248.0}, "add_rmsnorm": {1: 12.0},
+             "matmul_o_add_rmsnorm_relay": {4: 60.0}, "matmul_down_add_rmsnorm_relay": {"4": 265.0}}
+    edges, detail = P.relay_edges(table, 4, launch_us=2.0)
+    assert edges == ["o"]
+    assert detail["o"] == {"relay_us": 60.0, "unrelayed_us": 69.0, "gain_us": 9.0}
+    assert detail["down"]["gain_us"] == -3.0
+    assert P.relay_mode(table, 4, 2.0) == "relay_split:4:o"
+    # at k = 2 nothing is priced: no edge, mode "none"
+    assert P.relay_edges(table, 2) == ([], {})
+    assert P.relay_mode(table, 2) == "relay_split:2:none"
+    table["matmul_down_add_rmsnorm_relay"][4] = 200.0
+    assert P.relay_mode(table, 4, 2.0) == "relay_split:4:o+down"
