@@ -386,12 +386,12 @@ def main():
                 shutil.rmtree(t2, ignore_errors=True)
     if head["edges"]:
         workload = ("%s-shaped prefill, batch 1, seq %d: relay split at %d row tiles, flag edges %s -> "
-                    "Add+RMSNorm (%d flag blocks per prefill; chosen from this card's measured costs), SwiGLU "
+                    "Add+RMSNorm (%d flag blocks per prefill; the fastest edge subset replayed in place), SwiGLU "
                     "fused into the gate/up GEMM epilogue" % (PRESET_NAMES.get(args.preset, args.preset), S, k,
                                                                "+".join(head["edges"]), split["flag_edges"]))
     else:
         workload = ("%s-shaped prefill, batch 1, seq %d: relay split at %d row tiles with SwiGLU fused into the "
-                    "gate/up GEMM epilogue; no o/down flag edge pays on this card's measured costs, so none is "
+                    "gate/up GEMM epilogue; replayed in place, no o/down flag edge subset beat none, so none is "
                     "taken" % (PRESET_NAMES.get(args.preset, args.preset), S, k))
     out = {
         "metric": "Qwen2.5-7B prefill tok/s @seq2048 1 GPU; split-vs-serial speedup; MFMA util",
@@ -407,7 +407,11 @@ def main():
         "serial_ms_per_step": round(total_serial_s * 1e3 / args.steps, 3),
         "serial_tok_s": round(args.steps * S / total_serial_s, 1),
         "split_vs_serial": round(total_serial_s / total_split_s, 4),
-        "relay_edges": {"chosen": head["edges"], "priced": head["edge_costs"]},
+        # flag edges kept by the library after replaying every subset in
+        # place (tuned_us: best replay of each), and the planner's choice
+        # from the per-op profile (priced) for comparison
+        "relay_edges": {"chosen": head["edges"], "tuned_us": head["tuned_us"], "planned": head["planned_edges"],
+                        "priced": head["edge_costs"]},
         # makespan per program, each against serial
         "relay_breakdown": head["breakdown"],
         "best_ms": {"serial": round(serial["best_us"] / 1e3, 3), "split": round(split["best_us"] / 1e3, 3)},
@@ -472,10 +476,13 @@ def run_program(model_dir, name, mode, env, S, steps, warmup):
 
 def prefill_config(model_dir, preset, S, k, steps, warmup, ablation, dump_logits):
     """One prefill configuration: write its model directory (unless there),
-    price the flag edges, run serial (graph_whole) and the relay split with
-    the edges that pay (plus, with `ablation`, the split with no flag edge,
-    with both, and both without the SwiGLU fusion); every program's logits
-    must equal serial's bit for bit."""
+    run serial (graph_whole) and the relay split (relay_split:<k>: the
+    library builds the program with every subset of the o / down flag edges,
+    replays each in place and keeps the fastest), plus, with `ablation`, the
+    split with no flag edge, with both, and both without the SwiGLU fusion;
+    every program's logits must equal serial's bit for bit. The planner's
+    pricing of the same edges from the per-op profile is reported beside the
+    in-place choice."""
     import torch
 
     from kernrelay_amd import modeldir
@@ -487,37 +494,45 @@ def prefill_config(model_dir, preset, S, k, steps, warmup, ablation, dump_logits
         torch.cuda.synchronize()
         torch.cuda.empty_cache()
         log("model dir written in %.1f s" % (time.time() - t0))
-    edges, edge_costs = choose_edges(model_dir, S, k)
-    log("%s: relay edges priced %s -> %s" % (preset, json.dumps(edge_costs), edges or "none"))
-    split_mode = "relay_split:%d:%s" % (k, "+".join(edges) if edges else "none")
+    planned, edge_costs = choose_edges(model_dir, S, k)
+    log("%s: planner prices the relay edges %s -> %s" % (preset, json.dumps(edge_costs), planned or "none"))
+    split_mode = "relay_split:%d" % k
     timing = {"KR_TIME_OPS": "1"}
     dump = None
     split_env = dict(timing)
     if dump_logits:
         split_env["KR_DUMP_DIR"] = str(model_dir)
         dump = model_dir / "last_logits_bf16.bin"
-    plan = [("serial", "graph_whole", timing), ("split", split_mode, split_env)]
+    runs = {name: run_program(model_dir, name, mode, env, S, steps, warmup)
+            for name, mode, env in (("serial", "graph_whole", timing), ("split", split_mode, split_env))}
+    chosen = runs["split"]["relay_edges"]
+    log("%s: edges tuned in place %s -> %s" % (preset, json.dumps(runs["split"].get("relay_edges_tuned_us")), chosen))
     if ablation:
         # the split with no flag edge (the SwiGLU epilogue only), with both
         # flag edges, and both flag edges without the SwiGLU fusion
-        if edges:
+        plan = []
+        if chosen != "none":
             plan.append(("fusion_only", "relay_split:%d:none" % k, timing))
-        if edges != ["o", "down"]:
+        if chosen != "o+down":
             plan.append(("flag_relay_all", "relay_split:%d:o+down" % k, timing))
         plan.append(("flag_relay_only", "relay_split:%d:o+down" % k, dict(timing, KR_SPLIT_SWIGLU="kernel")))
-    runs = {name: run_program(model_dir, name, mode, env, S, steps, warmup) for name, mode, env in plan}
+        for name, mode, env in plan:
+            runs[name] = run_program(model_dir, name, mode, env, S, steps, warmup)
+        runs.setdefault("fusion_only", runs["split"])
+        runs.setdefault("flag_relay_all", runs["split"])
     for name, r in runs.items():
         if r["logits_fnv64"] != runs["serial"]["logits_fnv64"]:
             raise RuntimeError("%s: %s logits differ from serial" % (preset, name))
-    if "fusion_only" not in runs:
-        runs["fusion_only"] = runs["split"]
 
     def ms(r):
         return round(sum(r["samples_us"]) / len(r["samples_us"]) / 1e3, 3)
 
     breakdown = {name: {"ms_per_step": ms(r), "vs_serial": round(ms(runs["serial"]) / ms(r), 4),
-                        "flag_edges": r["flag_edges"]} for name, r in runs.items()}
-    return {"runs": runs, "edges": edges, "edge_costs": edge_costs, "split_mode": split_mode,
+                        "flag_edges": r["flag_edges"], "relay_edges": r.get("relay_edges")}
+                 for name, r in runs.items()}
+    edges = [] if chosen == "none" else chosen.split("+")
+    return {"runs": runs, "edges": edges, "edge_costs": edge_costs, "planned_edges": planned,
+            "tuned_us": runs["split"].get("relay_edges_tuned_us"), "split_mode": split_mode,
             "breakdown": breakdown, "dump": dump}
 
 
@@ -528,6 +543,7 @@ def config_summary(r, S):
     return {"serial_ms": round(ts / 1e3, 3), "split_ms": round(tp / 1e3, 3),
             "serial_tok_s": round(S * 1e6 / ts, 1), "split_tok_s": round(S * 1e6 / tp, 1),
             "split_vs_serial": round(ts / tp, 4), "split_mode": r["split_mode"], "relay_edges": r["edges"],
+            "relay_edges_tuned_us": r["tuned_us"], "relay_edges_planned": r["planned_edges"],
             "relay_edges_priced": r["edge_costs"], "flag_edges": split["flag_edges"],
             "flag_timeouts": split["flag_timeouts"], "argmax": split["argmax"], "bit_exact_serial_vs_split": True,
             "op_avg_us": split.get("op_avg_us")}

@@ -68,9 +68,12 @@ struct Mode {
     bool fused = false;    // fused Add+RMSNorm
     int tiles = 1;         // relay row tiles
     bool split = false;    // tile-released consumers with in-kernel waits
-    // relay_split flag edges (o -> Add+RMSNorm, down -> Add+RMSNorm); by
-    // default every edge whose relay tiles fit the device
+    // relay_split flag edges (o -> Add+RMSNorm, down -> Add+RMSNorm), named
+    // in the mode string; without a name (auto_edges) every subset whose
+    // relay tiles fit the device is built and timed in place and the fastest
+    // program is kept
     bool edge_o = true, edge_down = true;
+    bool auto_edges = false;
 };
 
 Mode ParseMode(const std::string &m)
@@ -93,6 +96,7 @@ Mode ParseMode(const std::string &m)
     } else if (m.rfind("relay_split", 0) == 0) {
         md.dual = md.flags = md.fused = md.graph = md.split = true;
         md.tiles = 4;
+        md.auto_edges = true;
         if (m.size() > 11) {
             // relay_split:<k>[:<edges>], edges = o+down | o | down | none
             if (m[11] != ':') throw std::runtime_error("unknown mode " + m);
@@ -103,6 +107,7 @@ Mode ParseMode(const std::string &m)
                 throw std::runtime_error("relay_split: tile count must be a number in 1..8");
             md.tiles = std::atoi(ks.c_str());
             if (colon != std::string::npos) {
+                md.auto_edges = false;
                 const std::string edges = rest.substr(colon + 1);
                 if (edges == "o+down" || edges == "down+o") {
                 } else if (edges == "o") {
@@ -178,9 +183,87 @@ public:
         Allocate();
         load_ms_ = Us(t0, Clock::now()) / 1000.0;
         if (program) {
+            if (mode_.split && mode_.auto_edges) TuneSplitEdges();
             BuildProgram();
             if (mode_.graph) Capture();
         }
+    }
+
+    // relay_split without named edges: the program is built and captured for
+    // every subset of the o and down flag edges whose relay tiles fit, each
+    // replayed (one warm-up, then 3 timed replays, over two passes in
+    // opposite orders so no candidate always runs first); the fastest
+    // subset is kept. Every candidate computes the same bits. Leaves the
+    // choice in mode_ and the timings in tuned_.
+    void TuneSplitEdges()
+    {
+        const int S = seq_, T = S / mode_.tiles;
+        if (S % mode_.tiles != 0 || T % 64 != 0)
+            throw std::runtime_error("relay_split: seq/tiles must be a multiple of 64");
+        const bool o_fits = GemmNormRelayFits(S, H_, HQ_ * D_, T, skws_bytes_ > 0);
+        const bool d_fits = GemmNormRelayFits(S, H_, I_, T, skws_bytes_ > 0);
+        std::vector<std::pair<bool, bool>> cands{{false, false}};
+        if (o_fits) cands.push_back({true, false});
+        if (d_fits) cands.push_back({false, true});
+        if (o_fits && d_fits) cands.push_back({true, true});
+        auto name = [](const std::pair<bool, bool> &c) {
+            return c.first ? (c.second ? std::string("o+down") : std::string("o"))
+                           : (c.second ? std::string("down") : std::string("none"));
+        };
+        tuned_.clear();
+        if (cands.size() > 1) {
+            std::vector<double> best(cands.size(), 1e300);
+            for (int pass = 0; pass < 2; ++pass) {
+                for (size_t j = 0; j < cands.size(); ++j) {
+                    const size_t i = pass == 0 ? j : cands.size() - 1 - j;
+                    ResetProgram();
+                    mode_.edge_o = cands[i].first;
+                    mode_.edge_down = cands[i].second;
+                    BuildProgram();
+                    Capture();
+                    RunOnce();
+                    Check(hipDeviceSynchronize(), "tune warm-up");
+                    for (int r = 0; r < 3; ++r) {
+                        Check(hipEventRecord(t0_, streams_.prod), "record");
+                        RunOnce();
+                        Check(hipEventRecord(tp_, streams_.prod), "record");
+                        Check(hipEventSynchronize(tp_), "tune sync");
+                        float ms = 0.f;
+                        Check(hipEventElapsedTime(&ms, t0_, tp_), "elapsed");
+                        best[i] = std::min(best[i], 1000.0 * ms);
+                    }
+                }
+            }
+            size_t pick = 0;
+            for (size_t i = 0; i < cands.size(); ++i) {
+                tuned_[name(cands[i])] = best[i];
+                if (best[i] < best[pick]) pick = i;
+            }
+            mode_.edge_o = cands[pick].first;
+            mode_.edge_down = cands[pick].second;
+        } else {
+            mode_.edge_o = mode_.edge_down = false;
+        }
+        ResetProgram();
+    }
+
+    // Drop a built program: graphs, launch list, relay blocks and timing events.
+    void ResetProgram()
+    {
+        Check(hipDeviceSynchronize(), "reset sync");
+        for (auto &g : graphs_) {
+            if (g.second) (void)hipGraphExecDestroy(g.second);
+            if (g.first) (void)hipGraphDestroy(g.first);
+        }
+        graphs_.clear();
+        for (auto &t : kev_) {
+            (void)hipEventDestroy(t.a);
+            (void)hipEventDestroy(t.b);
+        }
+        kev_.clear();
+        prog_.clear();
+        consumed_.clear();
+        ctrl_blocks_ = 0;
     }
 
     void RunOnce()
@@ -343,6 +426,14 @@ public:
             }
         }
         r.Set("last_top2_margin", Value::MakeNumber(margin_));
+        if (mode_.split) {
+            r.Set("relay_edges", Value::MakeString(edges_));
+            if (!tuned_.empty()) {
+                Value tv = Value::MakeObject();
+                for (const auto &kv : tuned_) tv.Set(kv.first, Value::MakeNumber(kv.second));
+                r.Set("relay_edges_tuned_us", tv);
+            }
+        }
         r.Set("consumer_cus", Value::MakeNumber(streams_.cons_cus));
         r.Set("load_ms", Value::MakeNumber(load_ms_));
         r.Set("kernels_per_run", Value::MakeNumber(double(prog_.size())));
@@ -889,6 +980,7 @@ private:
         const bool norm_env = EnvInt("KR_SPLIT_NORM", 1) != 0;
         const bool o_relay = norm_env && mode_.edge_o && GemmNormRelayFits(S, H_, HQ_ * D_, T, skws_bytes_ > 0);
         const bool d_relay = norm_env && mode_.edge_down && GemmNormRelayFits(S, H_, I_, T, skws_bytes_ > 0);
+        edges_ = o_relay ? (d_relay ? "o+down" : "o") : (d_relay ? "down" : "none");
         const int o_edge = o_relay ? NewEdge(k * L_) : 0;
         const int d_edge = d_relay ? NewEdge(k * L_) : 0;
         for (int b = 0; b < (o_relay ? k * L_ : 0); ++b) consumed_.push_back(o_edge + b);
@@ -1190,6 +1282,10 @@ private:
     std::vector<OpTiming> kev_;
     std::map<std::string, double> op_us_;
     std::map<std::string, int> op_n_;
+    // relay_split's flag edges as built, and each candidate's best replay
+    // (us) when they were tuned in place
+    std::string edges_;
+    std::map<std::string, double> tuned_;
     std::vector<double> samples_, host_samples_, dev_samples_;
     int argmax_ = -1, ref_argmax_ = -1, flag_edges_ = 0, flag_timeouts_ = 0;
     double maxdiff_ = -1.0, absmean_ = 0.0, margin_ = 0.0, load_ms_ = 0.0;

@@ -29,7 +29,8 @@ from tests.conftest import announce
 pytestmark = pytest.mark.gpu
 
 MODES = ["serial", "serial_fused", "serial_graph", "graph_whole", "relay_event", "relay_flag",
-         "relay_flag_graph", "relay_split:1", "relay_split:2", "relay_split:4"]
+         "relay_flag_graph", "relay_split:1", "relay_split:2", "relay_split:4", "relay_split:4:o+down",
+         "relay_split:2:none"]
 ATOL, RTOL = 2e-2, 1e-2
 # Two-layer model-shape tests (Qwen2.5-0.5B / 7B / Qwen3-8B sizes, ~152k
 # logits). The fp32 oracle's own logits move by more than 2e-2 under changes
@@ -38,12 +39,18 @@ ATOL, RTOL = 2e-2, 1e-2
 #                                   0.5B seed 3      7B seed 2
 #   GEMMs accumulated in fp64       0.0234 (0.0037)  0.0469 (0.0076)
 #   P rounded to bf16 before P.V    0.0234 (0.0039)  0.0625 (0.0092)
-# (max |d|, mean in brackets). The kernels accumulate in fp32 in their own
-# order and round P to bf16 for the MFMA, so the bound for these tests is
-# the larger of the two with room: 3e-2 (0.5B) and 8e-2 (7B, 8B) absolute
-# plus 1e-2 |ref|, and the mean deviation at most 1.5e-2. The argmax is
-# asserted with a margin above twice the largest deviation.
-MODEL_BOUND = {"qwen2.5-0.5b": 3e-2, "qwen2.5-7b": 8e-2, "qwen3-8b": 8e-2}
+# (max |d|, mean in brackets). Measured on MI355X, the GPU's logits against
+# the oracle (max |d|, mean; smallest absolute bound that passes with
+# 1e-2 |ref|): 0.5B 0.0234, 0.0040, 2e-2; 7B 0.0625, 0.0105, 6e-2; Qwen3-8B
+# (seq 4096, seed 1234) 0.0645, 0.0100, 6e-2. Against the oracle with P
+# rounded to bf16 before P.V (what the kernels' MFMA takes) they are the
+# same or larger (0.0254, 0.0625, 0.0664): the residue is the stored bf16
+# activations, each rounded after an fp32 sum taken in another order, not
+# the P rounding. So 0.5B holds the task's bar, 2e-2 absolute plus 1e-2
+# |ref|, and the 7B / 8B shapes 6e-2 absolute plus 1e-2 |ref|; the mean
+# deviation at most 1.5e-2 everywhere. The argmax is asserted with a margin
+# above twice the largest deviation.
+MODEL_BOUND = {"qwen2.5-0.5b": 2e-2, "qwen2.5-7b": 6e-2, "qwen3-8b": 6e-2}
 MODEL_MEAN = 1.5e-2
 
 
@@ -179,14 +186,16 @@ def test_qwen05_shapes_split_bit_exact(gpu, tmp_path):
     a = run(d, "graph_whole", seq, dump)
     check_logits(dump, ref, atol=MODEL_BOUND["qwen2.5-0.5b"], mean_tol=MODEL_MEAN)
     for k in (1, 2, 4, 8):
-        b = run(d, "relay_split:%d" % k, seq)
+        b = run(d, "relay_split:%d:o+down" % k, seq)
         assert a["logits_fnv64"] == b["logits_fnv64"], k
         assert b["flag_timeouts"] == 0
+    b = run(d, "relay_split:4", seq)  # edges chosen in place
+    assert a["logits_fnv64"] == b["logits_fnv64"] and b["relay_edges"] in b["relay_edges_tuned_us"]
     # the flag-released SwiGLU variant: SwiGLU workgroups appended to the
     # gate/up GEMM wait on its 4 row tiles
     os.environ["KR_SPLIT_SWIGLU"] = "flags"
     try:
-        c = run(d, "relay_split:4", seq)
+        c = run(d, "relay_split:4:o+down", seq)
     finally:
         del os.environ["KR_SPLIT_SWIGLU"]
     assert a["logits_fnv64"] == c["logits_fnv64"]
@@ -201,9 +210,16 @@ def _large_shapes(tmp_path, preset, seq, seed):
     check_logits(dump, ref, atol=MODEL_BOUND[preset], mean_tol=MODEL_MEAN)
     assert a["ref_argmax"] == ref["argmax"]
     for k in (1, 2, 4, 8):
-        b = run(d, "relay_split:%d" % k, seq, iters=1)
+        b = run(d, "relay_split:%d:o+down" % k, seq, iters=1)
         assert b["logits_fnv64"] == a["logits_fnv64"], k
         assert b["flag_timeouts"] == 0 and b["argmax"] == ref["argmax"]
+        assert b["relay_edges"] == "o+down" and b["flag_edges"] == 2 * 2 * k
+    # edges chosen in place: every candidate timed, the fastest kept, the same bits
+    c = run(d, "relay_split:4", seq, iters=1)
+    assert c["logits_fnv64"] == a["logits_fnv64"]
+    tuned = c["relay_edges_tuned_us"]
+    assert set(tuned) == {"none", "o", "down", "o+down"}
+    assert tuned[c["relay_edges"]] == min(tuned.values())
     return a
 
 
@@ -298,7 +314,7 @@ def test_full_depth_vs_transformers(gpu, tmp_path, preset):
     The deviation envelopes (FULL_DEPTH) are what bf16 activations
     accumulate over the layers: ~10 roundings a layer make a random walk of
     sqrt(10 L) x 2^-8 of the hidden state (7B: ~6% against a logit spread of
-    ~1.2, measured mean 0.075), where the two-layer tests hold 8e-2. Where
+    ~1.2, measured mean 0.075), where the two-layer tests hold 6e-2. Where
     transformers' top-2 margin is below the largest deviation (7B 0.045,
     0.5B 0.039) the argmax is decided by our deviation at its top logits,
     which the test reports (0.004 / 0.010 and 0.013 / 0.021)."""
@@ -315,27 +331,27 @@ def test_full_depth_vs_transformers(gpu, tmp_path, preset):
         ref = hf.write_reference(d, torch.float32, device="cuda")["last_logits"].double()
         torch.cuda.empty_cache()
         got = {}
-        for mode in ("graph_whole", "relay_split:4"):
+        for mode in ("graph_whole", "relay_split:4:o+down"):
             dump = tmp / ("dump_" + mode.replace(":", "_"))
             dump.mkdir()
             r = run(d, mode, seq, dump, iters=1)
             assert r["flag_timeouts"] == 0
             w = np.fromfile(dump / "last_logits_bf16.bin", dtype=np.uint16)
             got[mode] = (r, torch.from_numpy(w.view(np.int16).copy()).view(torch.bfloat16).double())
-        assert got["graph_whole"][0]["logits_fnv64"] == got["relay_split:4"][0]["logits_fnv64"]
-        assert got["relay_split:4"][0]["flag_edges"] > 0
+        assert got["graph_whole"][0]["logits_fnv64"] == got["relay_split:4:o+down"][0]["logits_fnv64"]
+        assert got["relay_split:4:o+down"][0]["flag_edges"] > 0
         top = torch.topk(ref, 3)
         # the runtime's own Verify against the written reference
-        rv = got["relay_split:4"][0]
+        rv = got["relay_split:4:o+down"][0]
         assert rv["ref_argmax"] == int(top.indices[0]) == rv["argmax"], (rv["ref_argmax"], rv["argmax"])
         assert rv["maxdiff"] is not None and rv["maxdiff"] <= max_tol, rv["maxdiff"]
-        g = got["relay_split:4"][1]
+        g = got["relay_split:4:o+down"][1]
         err = (g - ref).abs()
         announce("transformers argmax %d (margin %.4g); ours %d; max |d| %.4g, mean %.4g; |d| at the top three %s" % (
             int(top.indices[0]), float(top.values[0] - top.values[1]), int(g.argmax()), float(err.max()),
             float(err.mean()), [round(float(err[i]), 4) for i in top.indices]))
         assert int(g.argmax()) == int(top.indices[0])
-        assert got["relay_split:4"][0]["argmax"] == int(top.indices[0])
+        assert got["relay_split:4:o+down"][0]["argmax"] == int(top.indices[0])
         assert float(err.max()) <= max_tol and float(err.mean()) <= mean_tol, (float(err.max()), float(err.mean()))
     finally:
         import shutil
