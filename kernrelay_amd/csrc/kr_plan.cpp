@@ -328,6 +328,7 @@ public:
         if (sync_ != "flag" && sync_ != "event") throw std::runtime_error("KR_SYNC must be flag or event");
         wait_kind_ = EnvStr("KR_RELAY_WAIT", "fused");
         relay_grid_ = EnvInt("KR_RELAY_GRID", 256);
+        partition_ = std::max(0, EnvInt("KR_PLAN_PARTITION", 0));
         fan_max_ = EnvInt("KR_PLAN_FAN", kMaxFanOut);
         max_spins_ = uint32_t(EnvInt("KR_MAX_SPINS", int(kDefaultMaxSpins)));
         if (mode_ != "direct" && mode_ != "graph" && mode_ != "graph_per_stream" && mode_ != "graph_segment")
@@ -336,6 +337,9 @@ public:
         // graph_segment joins its graphs with events (the segments' waits and
         // publishes), whatever KR_SYNC says
         if (mode_ == "graph_segment") sync_ = "event";
+        // a CU partition needs the two lanes on their own queues at launch
+        // time; one multi-stream graph may run every node on one queue
+        if (mode_ == "graph" || sync_ != "flag") partition_ = 0;
     }
 
     ~Executor()
@@ -367,7 +371,15 @@ public:
         Check(hipDeviceGetAttribute(&ncu_, hipDeviceAttributeMultiprocessorCount, device_), "CU count");
         // a persistent consumer beside a GEMM: at most one workgroup per CU
         relay_grid_ = std::max(1, std::min(relay_grid_, ncu_));
-        streams_.Create(device_);
+        // KR_PLAN_PARTITION = n: lane 1 (the vector engine's lane) owns n CUs
+        // of every XCD and lane 0 the rest, as the reference's vector and
+        // cube cores are separate; the consumer grid is one workgroup per
+        // lane-1 CU
+        partition_ = std::min(partition_, ncu_ / 16);
+        streams_.Create(device_, partition_);
+        // there the lane-1 CUs are the consumer's alone: eight workgroups per
+        // CU keep enough loads in flight for a memory-bound pass on a few CUs
+        if (partition_ > 0) relay_grid_ = std::max(1, EnvInt("KR_RELAY_GRID", streams_.cons_cus * 8));
         Check(hipEventCreate(&ev0_), "event");
         Check(hipEventCreate(&ev1_), "event");
         Check(hipEventCreate(&ev2_), "event");
@@ -464,6 +476,7 @@ public:
     }
     const std::string &sync() const { return sync_; }
     int consumer_cus() const { return streams_.cons_cus; }
+    int partition() const { return partition_; }
 
 private:
     int64_t OutRows(const NodeSpec &n) const { return n.rows; }
@@ -693,6 +706,7 @@ private:
     // KR_PLAN_CORESIDENT=1 keeps co-resident tiles throughout.
     bool CoresidentPays(const Launch &L) const
     {
+        if (partition_ > 0) return false;  // its consumers run on CUs of their own
         if (EnvInt("KR_PLAN_CORESIDENT", 0) != 0) return true;
         const int64_t prows = L.pub_rows > 0 ? L.pub_rows : TaskRows(*L.task);
         const int N = int(L.task->n_tile > 0 ? L.task->n_tile : L.node->n);
@@ -752,6 +766,9 @@ private:
     int EarlyTiles(const Launch &PL, const Launch &L, int64_t in_off, int64_t in_rows) const
     {
         const NodeSpec &P = *PL.node;
+        // with a CU partition the consumer's persistent grid has CUs of its
+        // own: every tile waits in-kernel there
+        if (partition_ > 0) return -1;
         // a GEMM that leaves no room beside it: a persistent consumer grid
         // would hold the CUs its own rows need, so its consumers take the
         // one-wave wait kernel and run at full width after it
@@ -911,7 +928,13 @@ private:
                     if (k * prows < in_off + in_rows && (k + 1) * prows > in_off) hits.push_back(k);
                 const bool contiguous_adv =
                     adv.empty() || (adv.back() - adv.front() + 1 == int(adv.size()));
-                const bool fusable = wait_kind_ == "fused" && by_prod.size() == 1 && n.op != Op::MatMul &&
+                // a GEMM consumer waits in its own workgroups only when they
+                // cannot hold CUs its producer needs (a CU partition between
+                // the lanes); otherwise behind one-workgroup wait kernels
+                const bool gemm_ok =
+                    n.op != Op::MatMul ||
+                    (partition_ > 0 && L.fan.size() == 1 && launches_[launch_of.at({P.id, kv.second.front()})].lane != L.lane);
+                const bool fusable = wait_kind_ == "fused" && by_prod.size() == 1 && gemm_ok &&
                                      hits == kv.second && contiguous_adv;
                 if (fusable) {
                     L.fused_wait = true;
@@ -1123,6 +1146,9 @@ private:
             d.N = int(ncols);
             d.K = int(n.k);
             d.coresident = L.coresident;
+            // each workgroup waits for the producer tiles of the A rows it
+            // reads (a CU partition keeps it off the producer's CUs)
+            if (L.fused_wait) d.wait = L.wait;
             if (L.epi != nullptr) {
                 // the in-register relay: the consumer's rows leave with C's
                 const NodeSpec &c = *L.epi;
@@ -1323,6 +1349,7 @@ private:
     std::string wait_kind_;
     int relay_grid_ = 256;
     int ncu_ = 256;
+    int partition_ = 0;  // CUs per XCD owned by lane 1 (0: both lanes share every CU)
     int fan_max_ = kMaxFanOut;
     std::deque<TaskSpec> merged_;
     uint32_t max_spins_ = kDefaultMaxSpins;
@@ -1494,6 +1521,7 @@ int RunPlan(const char *schedule_json, int iters, int warmup, const char *device
         result.Set("flag_edges", Value::MakeNumber(ex.edges()));
         result.Set("epilogue_consumers", Value::MakeNumber(ex.epilogue_consumers()));
         result.Set("consumer_cus", Value::MakeNumber(ex.consumer_cus()));
+        result.Set("cu_partition_per_xcd", Value::MakeNumber(ex.partition()));
         json::WriteFile(out_json, result);
         std::printf("%s\n", result.Dump().c_str());
         std::fflush(stdout);

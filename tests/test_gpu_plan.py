@@ -308,6 +308,28 @@ def test_layernorm_to_gemm_relay(gpu, tmp_path, k):
     assert_close_to_oracle(schedule.serial_schedule(dag), outs, rows=128)
 
 
+@pytest.mark.parametrize("part", [1, 4])
+def test_cu_partition_bit_exact(gpu, tmp_path, part):
+    """KR_PLAN_PARTITION: lane 1 owns `part` CUs of every XCD and lane 0 the
+    rest. The consumers wait for each producer tile in persistent grids on
+    their own CUs, and a GEMM behind the other lane's producer waits in its
+    own workgroups (the reverse edge, and the second GEMM of mm -> GELU ->
+    mm -> GELU). Every node equals the serial program's bit for bit."""
+    ln = schedule.dag_from_dict({"name": "ln_mm", "nodes": [
+        {"name": "ln", "op": "layernorm", "engine": "aiv", "shape": {"rows": 4096, "cols": 2048}, "dtype": "bf16"},
+        {"name": "mm", "op": "matmul", "engine": "aic", "shape": {"M": 4096, "K": 2048, "N": 2048}, "dtype": "bf16"}],
+        "edges": [{"src": "ln", "dst": "mm", "kind": "data"}]})
+    for tag, dag in (("fanout", workloads.mm_fanout(tmp_path, 2048, 1024, 2048)), ("ln_mm", ln),
+                     ("chain2", workloads.e9_dag("e9_chain2", M=4096))):
+        _, base = run(schedule.serial_schedule(dag), tmp_path, tag + "_serial", iters=1, warmup=0)
+        r, outs = run(workloads.variants(dag, 4)["split"], tmp_path, "%s_p%d" % (tag, part), mode="graph_per_stream",
+                      env={"KR_PLAN_PARTITION": str(part)})
+        assert r["ok"] and r["gate_timeouts"] == 0, (tag, r)
+        assert r["cu_partition_per_xcd"] == part and r["consumer_cus"] == 8 * part, r
+        for node in base:
+            assert np.array_equal(base[node], outs[node]), (tag, part, node)
+
+
 def test_sync_micro_benchmark(gpu, tmp_path):
     """NHP_SYNC_BENCH (the reference's cross-stream sync micro-benchmark,
     exec/exec_main.cpp:751-833): 256 publish/wait kernel pairs per round on
