@@ -3,11 +3,16 @@
 // Replaces the reference's aclnnMatmul producer (exec/qwen_main.cpp:499-512,
 // exec/runtime/op_impl.cpp:175-201). Weights are re-laid out once at load as
 // Bt = weight_t^T ([N,K], K contiguous) so that both operands feed
-// v_mfma_f32_32x32x16_{bf16,f16} with one 16-byte load per lane.
+// v_mfma_f32_16x16x32_{bf16,f16} with one 16-byte load per lane.
 //
 // * 4 waves in a 2x2 grid (each wave owns (BM/2)x(BN/2) of C), or for
 //   256x256 tiles 8 waves in a 2x4 grid (128x64 each, two waves per SIMD), as
-//   32x32 accumulator blocks (fp32, 16 values per lane).
+//   32x32 accumulator blocks, each four 16x16 MFMA sub-blocks (fp32, 4
+//   values per lane each). The 16x16x32 instruction reads and writes a
+//   quarter of the accumulator registers of 32x32x16 per flop; under the
+//   card's power limit that measured ~10% more MFMA throughput at equal
+//   busy fraction (the 32x32 loop held 1.86-1.99 GHz, the 16x16 loop
+//   2.19-2.21 GHz).
 // * K is walked in 64-wide steps through a double-buffered LDS stage; global
 //   loads of step k+1 are in flight while step k runs on the matrix cores.
 // * LDS rows are 128 B (64 elements); the 16-byte chunk index is XOR-swizzled
@@ -15,8 +20,8 @@
 // * Every variant uses the same MFMA instruction and the same K order, so a
 //   row of C is bit-identical whatever BM/BN or row range a launch covers:
 //   the split schedule is bit-exact against the unsplit one.
-// * The MFMA is fed (B fragment, A fragment), so each 32x32 accumulator block
-//   holds C^T: every lane owns four runs of 4 consecutive columns of one row.
+// * The MFMA is fed (B fragment, A fragment), so each 16x16 sub-block holds
+//   C^T: lane l owns row l % 16 and columns 4 (l / 16) .. + 3 of it.
 // * Epilogue: acc -> 16-bit (RNE); with bias, bf16(bf16(acc)+bias) — the
 //   rounding of the reference's separate Matmul then Add (EmitQkv,
 //   exec/qwen_main.cpp:1336-1344). The tile is staged row-major in LDS
@@ -35,6 +40,7 @@ namespace {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 constexpr int kBK = 64;          // K elements per LDS stage
@@ -127,8 +133,29 @@ __device__ __forceinline__ void TileOf(int bid, int tiles_m, int tiles_n, int bm
     tn = r / gm;
 }
 
+// One 16x16x32 MFMA on a 16x16 sub-block: a holds 16 rows of the A operand
+// (lane l: row l % 16, k 8 (l / 16) .. + 7), b 16 columns of the B operand
+// likewise; c: lane l holds column l % 16, rows 4 (l / 16) .. + 3.
 template <int DT>
-__device__ __forceinline__ f32x16 Mfma(const uint4 &a, const uint4 &b, const f32x16 &c)
+__device__ __forceinline__ f32x4 Mfma(const uint4 &a, const uint4 &b, const f32x4 &c)
+{
+    if constexpr (DT == kBF16) {
+        return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
+                                                       __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+    } else {
+        return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a),
+                                                      __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+    }
+}
+
+// One 32x32x16 MFMA on a whole 32x32 block (the direct-to-LDS loop of the
+// 4-wave kernels, which measured faster with it): a and b hold 32 rows of
+// their operand (lane l: row l % 32, k 8 (l / 32) .. + 7); c: lane l holds
+// column l % 32, rows 8 (v / 4) + 4 (l / 32) + v % 4. For the same K order
+// it gives the same bits as four 16x16x32 MFMAs over the block's quarters
+// (the 7B prefill's logits hash is equal with either).
+template <int DT>
+__device__ __forceinline__ f32x16 Mfma32(const uint4 &a, const uint4 &b, const f32x16 &c)
 {
     if constexpr (DT == kBF16) {
         return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a),
@@ -137,6 +164,51 @@ __device__ __forceinline__ f32x16 Mfma(const uint4 &a, const uint4 &b, const f32
         return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a),
                                                       __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
     }
+}
+
+// Accumulator helpers over both layouts: block (i, j), four-value group c,
+// value e (the order stream-K partials are written and read back in).
+template <int MI, int NI>
+__device__ __forceinline__ void AccZero(f32x4 (&a)[MI][NI][4])
+{
+#pragma unroll
+    for (int i = 0; i < MI; ++i)
+#pragma unroll
+        for (int j = 0; j < NI; ++j)
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) a[i][j][q][e] = 0.0f;
+}
+template <int MI, int NI>
+__device__ __forceinline__ void AccZero(f32x16 (&a)[MI][NI])
+{
+#pragma unroll
+    for (int i = 0; i < MI; ++i)
+#pragma unroll
+        for (int j = 0; j < NI; ++j)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) a[i][j][e] = 0.0f;
+}
+template <int MI, int NI>
+__device__ __forceinline__ float AccAt(const f32x4 (&a)[MI][NI][4], int i, int j, int c, int e)
+{
+    return a[i][j][c][e];
+}
+template <int MI, int NI>
+__device__ __forceinline__ float AccAt(const f32x16 (&a)[MI][NI], int i, int j, int c, int e)
+{
+    return a[i][j][4 * c + e];
+}
+template <int MI, int NI>
+__device__ __forceinline__ void AccSet(f32x4 (&a)[MI][NI][4], int i, int j, int c, int e, float v)
+{
+    a[i][j][c][e] = v;
+}
+template <int MI, int NI>
+__device__ __forceinline__ void AccSet(f32x16 (&a)[MI][NI], int i, int j, int c, int e, float v)
+{
+    a[i][j][4 * c + e] = v;
 }
 
 // ---------------------------------------------------------------- tail
@@ -362,18 +434,56 @@ __device__ __forceinline__ void UnaryTile(const GemmParams &p, const uint16_t *s
     }
 }
 
-// Write the workgroup's BMxBN tile of C. acc[i][j] is the C^T block of rows
-// wm*BM/2 + 32i.., cols wn*BN/2 + 32j..: value v of lane l sits at row l%32,
-// col 8*(v/4) + 4*(l/32) + v%4. Each run of 4 columns goes to LDS as one
-// 8-byte write into a row-major tile whose 8-byte slots are XOR-swizzled with
-// row & 31 (32 rows of one column run hit 32 distinct bank pairs); then every
-// thread copies 16-byte row chunks to C (8 lanes cover a 128-byte line),
-// with device-scope stores when the launch releases relay tiles.
-// `stage` must hold BM*BN 16-bit values and be free (all waves past their
-// last LDS read of the main loop).
-template <int DT, int BM, int BN, int NT, int MI, int NI>
-__device__ __forceinline__ void StoreTile(const GemmParams &p, f32x16 (&acc)[MI][NI], uint16_t *stage, int m0,
-                                          int n0, int wm, int wn, int lane)
+// Stage the workgroup's BMxBN tile of C in LDS. acc[i][j][2 sn + sm] is the
+// C^T 16x16 sub-block of rows wm*BM/2 + 32i + 16sm.., cols wn*BN/2 + 32j +
+// 16sn..: value e of lane l sits at row l%16, col 4*(l/16) + e. Each run of
+// 4 columns goes to LDS as one 8-byte write into a row-major tile whose
+// 8-byte slots are XOR-swizzled with row & 31 (the rows of one column run hit
+// distinct bank pairs). `stage` must hold BM*BN 16-bit values and be free
+// (all waves past their last LDS read of the main loop).
+template <int DT, int BM, int BN, int MI, int NI>
+__device__ __forceinline__ void StageTile(const GemmParams &p, f32x4 (&acc)[MI][NI][4], uint16_t *stage, int n0, int wm,
+                                          int wn, int lane)
+{
+    constexpr int WTN = NI * 32;  // columns per wave
+    static_assert(BN >= 128, "slot swizzle needs >= 32 slots per row");
+    const int lr = lane & 15;         // row in a 16x16 sub-block
+    const int lc = 4 * (lane >> 4);   // first of the lane's four columns in it
+#pragma unroll
+    for (int j = 0; j < NI; ++j) {
+#pragma unroll
+        for (int sn = 0; sn < 2; ++sn) {
+            const int col = wn * WTN + j * 32 + 16 * sn + lc;
+            float b[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+            if (p.bias != nullptr) {
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    if (n0 + col + e < p.N) b[e] = Elem<DT>::Load(p.bias[n0 + col + e]);
+            }
+#pragma unroll
+            for (int i = 0; i < MI; ++i)
+#pragma unroll
+                for (int sm = 0; sm < 2; ++sm) {
+                    const int row = wm * (BM / 2) + i * 32 + 16 * sm + lr;
+                    uint32_t h[4];
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        const float x = acc[i][j][2 * sn + sm][e];
+                        h[e] = p.bias != nullptr ? Elem<DT>::Store(RoundTo<DT>(x) + b[e]) : Elem<DT>::Store(x);
+                    }
+                    const int slot = (col >> 2) ^ (row & 31);
+                    *reinterpret_cast<uint2 *>(stage + row * BN + slot * 4) =
+                        make_uint2(h[0] | (h[1] << 16), h[2] | (h[3] << 16));
+                }
+        }
+    }
+}
+
+// The same for a 32x32 accumulator block (lane l: row l % 32, four runs of
+// 4 consecutive columns 8 g + 4 (l / 32) ..).
+template <int DT, int BM, int BN, int MI, int NI>
+__device__ __forceinline__ void StageTile(const GemmParams &p, f32x16 (&acc)[MI][NI], uint16_t *stage, int n0, int wm,
+                                          int wn, int lane)
 {
     constexpr int WTN = NI * 32;  // columns per wave
     static_assert(BN >= 128, "slot swizzle needs >= 32 slots per row");
@@ -405,6 +515,16 @@ __device__ __forceinline__ void StoreTile(const GemmParams &p, f32x16 (&acc)[MI]
             }
         }
     }
+}
+
+// Write the workgroup's BMxBN tile of C: stage it, then every thread copies
+// 16-byte row chunks to C (8 lanes cover a 128-byte line), with
+// device-scope stores when the launch releases relay tiles.
+template <int DT, int BM, int BN, int NT, class ACC>
+__device__ __forceinline__ void StoreTile(const GemmParams &p, ACC &acc, uint16_t *stage, int m0, int n0, int wm,
+                                          int wn, int lane)
+{
+    StageTile<DT, BM, BN>(p, acc, stage, n0, wm, wn, lane);
     __syncthreads();
     constexpr int CPR = BN / 8;  // 16-byte chunks per row
     const bool vec = (p.ldc % 8 == 0) && ((reinterpret_cast<uintptr_t>(p.C) & 15) == 0);
@@ -469,16 +589,55 @@ __device__ __forceinline__ void StoreTile(const GemmParams &p, f32x16 (&acc)[MI]
 
 // SwiGLU epilogue: the in-register relay of the gate/up GEMM to its
 // consumer. C's columns hold gate and up interleaved in groups of 8 (cols
-// 16q..16q+7 gate, 16q+8..16q+15 up), so in each 32x32 C^T block a lane's
-// values v = 0..3 are gate columns 8g'+4h+e of group q (g' = 2q) and v = 4..7
-// the matching up columns (g' = 2q + 1): act[row, 8q + 4h + e] =
+// 16q..16q+7 gate, 16q+8..16q+15 up), so a 16x16 C^T sub-block is one group:
+// lanes 0-31 hold its gate columns 4 (l / 16) + e, lanes 32-63 the matching
+// up columns of the same rows. One v_permlane32_swap per value pairs them
+// (lanes 0-31 then hold gate and up of the sub-block's rows 0-15 of sm = 0,
+// lanes 32-63 those of sm = 1): act[row, 8q + 4 ((l / 16) & 1) + e] =
 // bf16(bf16(silu(bf16(gate))) * bf16(up)), the rounding of the standalone
 // SwiGLU kernel reading the stored gate/up tile. C itself is not written.
 // The BM x BN/2 act tile is staged in LDS like StoreTile's and leaves as
 // full-line 16-byte stores.
-template <int DT, int BM, int BN, int NT, int MI, int NI>
-__device__ __forceinline__ void StoreTileSwiglu(const GemmParams &p, f32x16 (&acc)[MI][NI], uint16_t *stage, int m0,
-                                                int n0, int wm, int wn, int lane)
+template <int DT, int BM, int BN, int MI, int NI>
+__device__ __forceinline__ void StageSwiglu(f32x4 (&acc)[MI][NI][4], uint16_t *stage, int wm, int wn, int lane)
+{
+    constexpr int AW = BN / 2;  // act columns of the tile
+    constexpr int WTA = NI * 16;  // act columns per wave
+    static_assert(AW >= 128, "slot swizzle needs >= 32 slots per row");
+    const int lr = lane & 15;
+    const int hi = lane >> 5;                // after the swap: sub-block rows 16 hi ..
+    const int lc = 4 * ((lane >> 4) & 1);    // first act column of the lane in its group
+#pragma unroll
+    for (int j = 0; j < NI; ++j) {
+#pragma unroll
+        for (int sn = 0; sn < 2; ++sn) {
+            const int acol = wn * WTA + j * 16 + 8 * sn + lc;
+#pragma unroll
+            for (int i = 0; i < MI; ++i) {
+                const int row = wm * (BM / 2) + i * 32 + 16 * hi + lr;
+                uint32_t h[4];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(acc[i][j][2 * sn][e]),
+                                                                     __float_as_uint(acc[i][j][2 * sn + 1][e]), false,
+                                                                     false);
+                    const float g = RoundTo<DT>(__uint_as_float(sw[0]));
+                    const float u = RoundTo<DT>(__uint_as_float(sw[1]));
+                    h[e] = Elem<DT>::Store(RoundTo<DT>(Silu(g)) * u);
+                }
+                const int slot = (acol >> 2) ^ (row & 31);
+                *reinterpret_cast<uint2 *>(stage + row * AW + slot * 4) =
+                    make_uint2(h[0] | (h[1] << 16), h[2] | (h[3] << 16));
+            }
+        }
+    }
+}
+
+// The same for 32x32 accumulator blocks: a lane's values v = 0..3 are gate
+// columns 8g'+4h+e of group q (g' = 2q) and v = 4..7 the matching up
+// columns (g' = 2q + 1), so no lane exchange is needed.
+template <int DT, int BM, int BN, int MI, int NI>
+__device__ __forceinline__ void StageSwiglu(f32x16 (&acc)[MI][NI], uint16_t *stage, int wm, int wn, int lane)
 {
     constexpr int AW = BN / 2;  // act columns of the tile
     constexpr int WTA = NI * 16;  // act columns per wave
@@ -506,6 +665,14 @@ __device__ __forceinline__ void StoreTileSwiglu(const GemmParams &p, f32x16 (&ac
             }
         }
     }
+}
+
+template <int DT, int BM, int BN, int NT, class ACC>
+__device__ __forceinline__ void StoreTileSwiglu(const GemmParams &p, ACC &acc, uint16_t *stage, int m0, int n0, int wm,
+                                                int wn, int lane)
+{
+    constexpr int AW = BN / 2;  // act columns of the tile
+    StageSwiglu<DT, BM, BN>(acc, stage, wm, wn, lane);
     __syncthreads();
     constexpr int CPR = AW / 8;
     const int64_t a0 = n0 / 2;
@@ -597,45 +764,56 @@ GemmKernel(GemmParams p)
         }
     };
 
-    f32x16 acc[MI][NI];
+    f32x4 acc[MI][NI][4];
 #pragma unroll
     for (int i = 0; i < MI; ++i)
 #pragma unroll
         for (int j = 0; j < NI; ++j)
 #pragma unroll
-            for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
+            for (int q = 0; q < 4; ++q)
+#pragma unroll
+                for (int v = 0; v < 4; ++v) acc[i][j][q][v] = 0.0f;
 
     const int nk = (p.K + kBK - 1) / kBK;
     load_global(0);
     store_lds(0);
     __syncthreads();
 
-    const int frow = lane & 31;
-    const int fhalf = lane >> 5;
+    const int frow = lane & 15;
+    const int fq = lane >> 4;
 
     for (int kt = 0; kt < nk; ++kt) {
         const int cur = kt & 1;
         if (kt + 1 < nk) load_global(kt + 1);
         const uint16_t *As = smem + cur * STAGE;
         const uint16_t *Bs = As + BM * kBK;
+        // two k32 steps: lane l reads row l % 16 of each 16-row fragment,
+        // 16-byte chunk 4 ks + l / 16
 #pragma unroll
-        for (int ks = 0; ks < kBK / 16; ++ks) {
-            const int chunk = ks * 2 + fhalf;
-            uint4 fa[MI], fb[NI];
-#pragma unroll
-            for (int i = 0; i < MI; ++i) {
-                const int r = wm * (BM / 2) + i * 32 + frow;
-                fa[i] = *reinterpret_cast<const uint4 *>(As + r * kBK + Swz(r, chunk) * 8);
-            }
-#pragma unroll
-            for (int j = 0; j < NI; ++j) {
-                const int r = wn * (BN / 2) + j * 32 + frow;
-                fb[j] = *reinterpret_cast<const uint4 *>(Bs + r * kBK + Swz(r, chunk) * 8);
-            }
+        for (int ks = 0; ks < kBK / 32; ++ks) {
+            const int chunk = ks * 4 + fq;
+            uint4 fa[MI][2], fb[NI][2];
 #pragma unroll
             for (int i = 0; i < MI; ++i)
 #pragma unroll
-                for (int j = 0; j < NI; ++j) acc[i][j] = Mfma<DT>(fb[j], fa[i], acc[i][j]);
+                for (int sm = 0; sm < 2; ++sm) {
+                    const int r = wm * (BM / 2) + i * 32 + 16 * sm + frow;
+                    fa[i][sm] = *reinterpret_cast<const uint4 *>(As + r * kBK + Swz(r, chunk) * 8);
+                }
+#pragma unroll
+            for (int j = 0; j < NI; ++j)
+#pragma unroll
+                for (int sn = 0; sn < 2; ++sn) {
+                    const int r = wn * (BN / 2) + j * 32 + 16 * sn + frow;
+                    fb[j][sn] = *reinterpret_cast<const uint4 *>(Bs + r * kBK + Swz(r, chunk) * 8);
+                }
+#pragma unroll
+            for (int i = 0; i < MI; ++i)
+#pragma unroll
+                for (int j = 0; j < NI; ++j)
+#pragma unroll
+                    for (int q = 0; q < 4; ++q)
+                        acc[i][j][q] = Mfma<DT>(fb[j][q >> 1], fa[i][q & 1], acc[i][j][q]);
         }
         if (kt + 1 < nk) store_lds(cur ^ 1);
         __syncthreads();
@@ -814,6 +992,16 @@ GemmFn PickGemmKernel(int K, bool sk, int &threads)
                     threads = 512;
                     return MainLoopMode() == 2 ? GemmPipeKernel<DT, BM, BN, 0, 8, false, 2>
                                                : GemmPipeKernel<DT, BM, BN, 0, 8>;
+                }
+            }
+            if constexpr (BM == 256 && BN == 128) {
+                static const bool staged = [] {
+                    const char *e = std::getenv("KR_GEMM_STAGED128");
+                    return e != nullptr && std::atoi(e) == 1;
+                }();
+                if (staged && MainLoopMode() == 2) {
+                    threads = 512;
+                    return GemmPipeKernel<DT, BM, BN, 0, 8, false, 2>;
                 }
             }
             threads = kThreads;
