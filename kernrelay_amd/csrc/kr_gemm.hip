@@ -994,16 +994,6 @@ GemmFn PickGemmKernel(int K, bool sk, int &threads)
                                                : GemmPipeKernel<DT, BM, BN, 0, 8>;
                 }
             }
-            if constexpr (BM == 256 && BN == 128) {
-                static const bool staged = [] {
-                    const char *e = std::getenv("KR_GEMM_STAGED128");
-                    return e != nullptr && std::atoi(e) == 1;
-                }();
-                if (staged && MainLoopMode() == 2) {
-                    threads = 512;
-                    return GemmPipeKernel<DT, BM, BN, 0, 8, false, 2>;
-                }
-            }
             threads = kThreads;
             switch (PrefetchStages()) {
             case 2: return GemmPipeKernel<DT, BM, BN, 2, 4>;
