@@ -47,8 +47,8 @@ def log(msg):
 # what the same counter reads for a plain 512 MiB device copy; and rocprof's
 # MFMA utilisation of the same launches (SQ_VALU_MFMA_BUSY_CYCLES over
 # GRBM_GUI_ACTIVE x SIMDs, at the clock the card ran).
-GATE_UP_TRAFFIC_BYTES = (423136.0 * 2.0 + 75776.0 * 1.0) * 1024
-GATE_UP_MFMA_UTIL = 0.635
+GATE_UP_TRAFFIC_BYTES = (423154.0 * 2.0 + 75776.0 * 1.0) * 1024
+GATE_UP_MFMA_UTIL = 0.627
 GATE_UP_TRAFFIC_SOURCE = "profiles/gemm_gate_up_swiglu_2048x37888x3584.md"
 
 

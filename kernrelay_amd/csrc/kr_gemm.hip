@@ -2,26 +2,32 @@
 //
 // Replaces the reference's aclnnMatmul producer (exec/qwen_main.cpp:499-512,
 // exec/runtime/op_impl.cpp:175-201). Weights are re-laid out once at load as
-// Bt = weight_t^T ([N,K], K contiguous) so that both operands feed
-// v_mfma_f32_16x16x32_{bf16,f16} with one 16-byte load per lane.
+// Bt = weight_t^T ([N,K], K contiguous) so that both operands feed the MFMA
+// with one 16-byte load per lane.
 //
 // * 4 waves in a 2x2 grid (each wave owns (BM/2)x(BN/2) of C), or for
 //   256x256 tiles 8 waves in a 2x4 grid (128x64 each, two waves per SIMD), as
-//   32x32 accumulator blocks, each four 16x16 MFMA sub-blocks (fp32, 4
-//   values per lane each). The 16x16x32 instruction reads and writes a
-//   quarter of the accumulator registers of 32x32x16 per flop; under the
-//   card's power limit that measured ~10% more MFMA throughput at equal
-//   busy fraction (the 32x32 loop held 1.86-1.99 GHz, the 16x16 loop
-//   2.19-2.21 GHz).
+//   32x32 accumulator blocks (fp32). The 8-wave register-staged kernels and
+//   the simple kernel compute a block as four 16x16 sub-blocks with
+//   v_mfma_f32_16x16x32 (4 values per lane each); the 4-wave direct-to-LDS
+//   kernels as one block with v_mfma_f32_32x32x16 (16 values per lane). The
+//   16x16x32 instruction reads and writes a quarter of the accumulator
+//   registers of 32x32x16 per flop; under the card's power limit an
+//   MFMA-only loop of it held 2.31 GHz against 1.95-2.10 GHz at the same
+//   busy fraction (kernrelay_amd/probes/mfma_power.hip).
 // * K is walked in 64-wide steps through a double-buffered LDS stage; global
 //   loads of step k+1 are in flight while step k runs on the matrix cores.
 // * LDS rows are 128 B (64 elements); the 16-byte chunk index is XOR-swizzled
-//   with (row>>1)&7 so a quarter-wave's ds_read_b128 hits distinct banks.
-// * Every variant uses the same MFMA instruction and the same K order, so a
-//   row of C is bit-identical whatever BM/BN or row range a launch covers:
-//   the split schedule is bit-exact against the unsplit one.
-// * The MFMA is fed (B fragment, A fragment), so each 16x16 sub-block holds
-//   C^T: lane l owns row l % 16 and columns 4 (l / 16) .. + 3 of it.
+//   with (row>>1)&7, under which the 16 lanes of a fragment read (16
+//   consecutive rows, one chunk) hit distinct banks (0 conflict cycles
+//   measured by kernrelay_amd/probes/lds_banks.hip).
+// * Every variant walks K in the same order, and the two MFMA shapes give
+//   the same bits for the same K order, so a row of C is bit-identical
+//   whatever BM/BN or row range a launch covers: the split schedule is
+//   bit-exact against the unsplit one.
+// * The MFMA is fed (B fragment, A fragment), so each block holds C^T: in a
+//   16x16 sub-block lane l owns row l % 16 and columns 4 (l / 16) .. + 3, in
+//   a 32x32 block row l % 32 and four runs of 4 columns.
 // * Epilogue: acc -> 16-bit (RNE); with bias, bf16(bf16(acc)+bias) — the
 //   rounding of the reference's separate Matmul then Add (EmitQkv,
 //   exec/qwen_main.cpp:1336-1344). The tile is staged row-major in LDS
