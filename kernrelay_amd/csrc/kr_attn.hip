@@ -261,21 +261,39 @@ AttnKernel(AttnParams p)
         }
     }
 
-    // S^T of one block: 2 halves of 32 keys
+    // S^T of one block: 2 halves of 32 keys. The K fragments of d step dc
+    // are read KAH steps ahead of their MFMA pair (a rolling window of KAH
+    // pairs in flight): left to itself the scheduler reuses one pair of
+    // registers and waits out the LDS latency before every pair.
     auto qk = [&](const uint16_t *K, f32x16 (&sacc)[2]) {
-        uint4 kf[2][D / 16];
-#pragma unroll
-        for (int dc = 0; dc < D / 16; ++dc)
+        constexpr int NP = D / 16;
+        constexpr int KAH = NP < 3 ? NP : 3;
+        uint4 kf[2][NP];
+        auto rd = [&](int dc) {
 #pragma unroll
             for (int kh = 0; kh < 2; ++kh) kf[kh][dc] = *reinterpret_cast<const uint4 *>(K + kh * 32 * D + kaddr[dc]);
+        };
+#pragma unroll
+        for (int dc = 0; dc < KAH; ++dc) rd(dc);
 #pragma unroll
         for (int kh = 0; kh < 2; ++kh)
 #pragma unroll
             for (int v = 0; v < 16; ++v) sacc[kh][v] = 0.0f;
 #pragma unroll
-        for (int dc = 0; dc < D / 16; ++dc)
+        for (int dc = 0; dc < NP; ++dc) {
 #pragma unroll
             for (int kh = 0; kh < 2; ++kh) sacc[kh] = Mfma<DT>(kf[kh][dc], qf[dc], sacc[kh]);
+            if (dc + KAH < NP) rd(dc + KAH);
+        }
+        // issue order: KAH read pairs, then (MFMA pair, read pair), then the
+        // last KAH MFMA pairs (0x100 DS read, 0x008 MFMA)
+        __builtin_amdgcn_sched_group_barrier(0x100, 2 * KAH, 0);
+#pragma unroll
+        for (int i = 0; i < NP - KAH; ++i) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+            __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+        }
+        __builtin_amdgcn_sched_group_barrier(0x008, 2 * KAH, 0);
     };
     // causal / past-S mask of one block's raw scores: register v of half kh
     // holds key kv0 + kh*32 + 8 (v/4) + 4 hf + v%4, masked to -inf when that
