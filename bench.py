@@ -158,14 +158,18 @@ def cpu_baseline(model_dir, gpu_last_logits=None):
            "sample": "oracle fp32 torch-CPU, the whole prefill: %d decoder layers + lm_head over all %d rows "
                      "at seq %d, weights converted from the model directory's bf16 as each op runs" % (m.L, S, S),
            "ms_per_prefill": round(total * 1e3, 1), "oracle_argmax": res["argmax"],
-           "oracle_top2_margin": round(res["margin"], 5)}
+           "oracle_top2_margin": round(res["margin"], 5),
+           "oracle_argmax_fp32": res["argmax_fp32"], "oracle_top2_margin_fp32": round(res["margin_fp32"], 5)}
     if gpu_last_logits is not None:
         ref = res["last_logits"].float()
         gpu = torch.from_numpy(np.asarray(gpu_last_logits, dtype=np.float32))
         d = (gpu - ref).abs()
+        g2 = torch.topk(gpu, 2)
         out["gpu_vs_oracle"] = {"max_abs": round(float(d.max()), 5), "mean_abs": round(float(d.mean()), 6),
                                 "argmax_equal": int(gpu.argmax()) == res["argmax"],
-                                "gpu_argmax": int(gpu.argmax())}
+                                "argmax_equal_fp32": int(gpu.argmax()) == res["argmax_fp32"],
+                                "gpu_argmax": int(gpu.argmax()),
+                                "gpu_top2_margin": round(float(g2.values[0] - g2.values[1]), 5)}
     return out
 
 

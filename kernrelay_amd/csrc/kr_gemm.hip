@@ -1066,14 +1066,17 @@ bool NormRelayResident(int dt, int bm, int bn, int M, int N, int K, int rows_per
 // Default: an exact split of K over 256x256 tiles, S = CUs / tiles pieces per
 // tile, each piece at least 16 K stages (S >= 2), so every workgroup runs one
 // piece and the workgroups of an XCD walk K in step on a compact patch of
-// tiles; only where the best data-parallel tiling fills less than 60% of the
-// device's workgroup slots. The last piece to finish sums all S partials
-// alone, so short pieces lose to that fix-up. Measured on MI355X with a warm
-// activation: 2048x896x4864 data-parallel 67.1 us (best tile), 2 pieces 65.7,
-// 4 pieces (19 stages) 53.6, 8 pieces (9.5 stages) 78.2; 2048x896x896 with 2
-// pieces of 7 stages 32.3 against 21.0; 2048x3584x18944 (the data-parallel
-// 256x128 tiles fill 87.5%) stays data-parallel: 245 us against 257 us split
-// in the prefill. Spreading the iterations of every tile over all 256 CUs
+// tiles; where the best data-parallel tiling fills less than 60% of the
+// device's workgroup slots, or less than 90% with K of at least 256 stages
+// (16384), where two long pieces per 256x256 tile amortise the fix-up. The
+// last piece to finish sums all S partials alone, so short pieces lose to
+// that fix-up. Measured on MI355X with a warm activation: 2048x896x4864
+// data-parallel 67.1 us (best tile), 2 pieces 65.7, 4 pieces (19 stages)
+// 53.6, 8 pieces (9.5 stages) 78.2; 2048x896x896 with 2 pieces of 7 stages
+// 32.3 against 21.0. 2048x3584x18944 (the data-parallel 256x128 tiles fill
+// 87.5%): 226 us in two pieces of 148 stages against 248 us data-parallel in
+// the 7B prefill, on the 16x16x32 staged loop (KR_GEMM_SK_LONGK=0 keeps it
+// data-parallel). Spreading the iterations of every tile over all 256 CUs
 // instead (pieces of uneven length at different K offsets, sharing no
 // operand lines) took 369 us for 2048x3584x18944. KR_GEMM_SK_WGS=G forces that
 // even spread over G workgroups (a measurement aid).
@@ -1090,7 +1093,12 @@ bool PlanStreamK(int M, int N, int K, StreamKPlan &pl)
         const int dp_tiles = ((M + dp.bm - 1) / dp.bm) * ((N + dp.bn - 1) / dp.bn);
         const int dp_slots = CuCount() * (dp.bm * dp.bn >= 256 * 128 ? 1 : 2);
         const int dp_rounds = (dp_tiles + dp_slots - 1) / dp_slots;
-        if (double(dp_tiles) / (double(dp_rounds) * dp_slots) >= 0.6) return false;
+        const double fill = double(dp_tiles) / (double(dp_rounds) * dp_slots);
+        static const bool longk = [] {
+            const char *e = std::getenv("KR_GEMM_SK_LONGK");
+            return e == nullptr || std::atoi(e) != 0;
+        }();
+        if (fill >= 0.6 && !(longk && fill < 0.9 && pl.nk >= 256)) return false;
         const int S = std::min(CuCount() / pl.tiles, pl.nk / 16);
         if (S < 2) return false;
         pl.G = S * pl.tiles;

@@ -61,13 +61,19 @@ def shape_bytes(node):
     return 4 * s.get("rows", 0) * s.get("cols", 0)
 
 
-def layer_dag(cfg, seq):
+def layer_dag(cfg, seq, fused=False):
     """Qwen prefill as the planner sees it (optimize.py:59-142).
 
     ``cfg`` holds the manifest config keys (hidden_size, intermediate_size,
     num_hidden_layers, num_attention_heads, num_key_value_heads, vocab_size,
     head_dim, qk_norm).  GEMMs run on engine ``aic``, vector ops on ``aiv``
     and attention on ``aicore`` (it occupies both).
+
+    ``fused=False`` is the reference's program: separate q/k/v projections,
+    RoPE, gate and up projections, SiLU and Mul.  ``fused=True`` is the
+    program this runtime launches: one QKV projection (its epilogue adds the
+    bias and, without q/k norms, applies RoPE), one gate/up projection whose
+    epilogue writes SwiGLU, then down.
     """
     H, I = cfg["hidden_size"], cfg["intermediate_size"]
     L, V = cfg["num_hidden_layers"], cfg["vocab_size"]
@@ -92,39 +98,59 @@ def layer_dag(cfg, seq):
         p = "l%d." % l
         node(p + "ln1", "rmsnorm", "aiv", rows=seq, cols=H)
         dep(prev, p + "ln1")
-        mm(p + "q", seq, H, HQ * D)
-        mm(p + "k", seq, H, HKV * D)
-        mm(p + "v", seq, H, HKV * D)
-        for x in "qkv":
-            dep(p + "ln1", p + x)
-        qsrc = p + "q"
-        if qk:
-            node(p + "qk_norm", "rmsnorm", "aiv", rows=seq * HQ, cols=D)
-            dep(p + "q", p + "qk_norm")
-            dep(p + "k", p + "qk_norm")
-            qsrc = p + "qk_norm"
-        node(p + "rope", "rope", "aiv", rows=seq, cols=HQ * D)
-        dep(qsrc, p + "rope")
-        node(p + "attn", "attention", "aicore", batch=1, q_heads=HQ,
-             kv_heads=HKV, seq=seq, head_dim=D)
-        dep(p + "rope", p + "attn")
-        dep(p + "v", p + "attn")
+        if fused:
+            mm(p + "qkv", seq, H, (HQ + 2 * HKV) * D)
+            dep(p + "ln1", p + "qkv")
+            asrc = p + "qkv"
+            if qk:
+                node(p + "qk_norm", "rmsnorm", "aiv", rows=seq * HQ, cols=D)
+                dep(p + "qkv", p + "qk_norm")
+                node(p + "rope", "rope", "aiv", rows=seq, cols=HQ * D)
+                dep(p + "qk_norm", p + "rope")
+                asrc = p + "rope"
+            node(p + "attn", "attention", "aicore", batch=1, q_heads=HQ,
+                 kv_heads=HKV, seq=seq, head_dim=D)
+            dep(asrc, p + "attn")
+        else:
+            mm(p + "q", seq, H, HQ * D)
+            mm(p + "k", seq, H, HKV * D)
+            mm(p + "v", seq, H, HKV * D)
+            for x in "qkv":
+                dep(p + "ln1", p + x)
+            qsrc = p + "q"
+            if qk:
+                node(p + "qk_norm", "rmsnorm", "aiv", rows=seq * HQ, cols=D)
+                dep(p + "q", p + "qk_norm")
+                dep(p + "k", p + "qk_norm")
+                qsrc = p + "qk_norm"
+            node(p + "rope", "rope", "aiv", rows=seq, cols=HQ * D)
+            dep(qsrc, p + "rope")
+            node(p + "attn", "attention", "aicore", batch=1, q_heads=HQ,
+                 kv_heads=HKV, seq=seq, head_dim=D)
+            dep(p + "rope", p + "attn")
+            dep(p + "v", p + "attn")
         mm(p + "o", seq, HQ * D, H)
         dep(p + "attn", p + "o")
         node(p + "addnorm1", "add_rmsnorm", "aiv", rows=seq, cols=H)
         dep(prev, p + "addnorm1")
         dep(p + "o", p + "addnorm1")
-        mm(p + "gate", seq, H, I)
-        mm(p + "up", seq, H, I)
-        dep(p + "addnorm1", p + "gate")
-        dep(p + "addnorm1", p + "up")
-        node(p + "silu", "silu", "aiv", rows=seq, cols=I)
-        dep(p + "gate", p + "silu")
-        node(p + "mul", "mul", "aiv", rows=seq, cols=I)
-        dep(p + "silu", p + "mul")
-        dep(p + "up", p + "mul")
-        mm(p + "down", seq, I, H)
-        dep(p + "mul", p + "down")
+        if fused:
+            mm(p + "gate_up", seq, H, 2 * I)
+            dep(p + "addnorm1", p + "gate_up")
+            mm(p + "down", seq, I, H)
+            dep(p + "gate_up", p + "down")
+        else:
+            mm(p + "gate", seq, H, I)
+            mm(p + "up", seq, H, I)
+            dep(p + "addnorm1", p + "gate")
+            dep(p + "addnorm1", p + "up")
+            node(p + "silu", "silu", "aiv", rows=seq, cols=I)
+            dep(p + "gate", p + "silu")
+            node(p + "mul", "mul", "aiv", rows=seq, cols=I)
+            dep(p + "silu", p + "mul")
+            dep(p + "up", p + "mul")
+            mm(p + "down", seq, I, H)
+            dep(p + "mul", p + "down")
         node(p + "addnorm2", "add_rmsnorm", "aiv", rows=seq, cols=H)
         dep(p + "addnorm1", p + "addnorm2")
         dep(p + "down", p + "addnorm2")
@@ -862,6 +888,11 @@ PROFILE_OPS = ("embedding", "rmsnorm", "add", "add_rmsnorm", "rope",
                "matmul_lm")
 
 
+# the fused projections of ``layer_dag(..., fused=True)`` (QKV with its bias /
+# RoPE epilogue, gate/up with its SwiGLU epilogue), timed as plain GEMMs
+FUSED_PROFILE_OPS = ("matmul_qkv", "matmul_gate_up")
+
+
 # the relay split's flag edges, each timed as one relayed launch (the GEMM
 # releasing k row tiles, its own workgroups running Add+RMSNorm on each) next
 # to the same work unrelayed (the GEMM, then the Add+RMSNorm kernel)
@@ -909,7 +940,7 @@ def profile_op(node):
     (optimize.py:193-207)."""
     if node["op"] == "matmul":
         tail = node["name"].rsplit(".", 1)[-1]
-        if tail in ("q", "k", "v", "o", "gate", "up", "down"):
+        if tail in ("q", "k", "v", "o", "gate", "up", "down", "qkv", "gate_up"):
             return "matmul_" + tail
         return "matmul_lm" if tail == "lm_head" else "matmul"
     return node["op"]

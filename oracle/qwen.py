@@ -94,7 +94,9 @@ def layer_forward(m, l, h, x, cos, sin, p_dt=None):
 
 def prefill(model_dir, layers=None, threads=None, lm_all_rows=False, p_dt=None):
     """Run the prefill; returns dict(last_logits=fp32 [V] of bf16 values,
-    argmax, margin). `layers` truncates the stack (tests of the CPU cost).
+    argmax, margin, and argmax_fp32 / margin_fp32 of the last row's product
+    before its bf16 rounding, where top logits can tie). `layers` truncates
+    the stack (tests of the CPU cost).
     lm_all_rows: compute the lm_head over every row, as the reference's
     prefill does (qwen_main.cpp:920, :989), instead of the last row only
     (the work of a timed baseline; the last row then differs from the
@@ -116,9 +118,11 @@ def prefill(model_dir, layers=None, threads=None, lm_all_rows=False, p_dt=None):
             gname = ("L%02d.input_layernorm.weight" % (l + 1)) if l + 1 < L else "final_norm.weight"
             x, h, _ = ops.add_rmsnorm(h2, d, m.tensor(gname), m.eps)
         logits = ops.gemm(x if lm_all_rows else x[-1:], m.tensor("lm_head.weight_t"))[-1]
-    top = torch.topk(logits, 2)
+        l32 = ops.gemm(x[-1:], m.tensor("lm_head.weight_t"), dt=torch.float32)[-1]
+    top, top32 = torch.topk(logits, 2), torch.topk(l32, 2)
     return {"last_logits": logits, "argmax": int(top.indices[0]),
-            "margin": float(top.values[0] - top.values[1])}
+            "margin": float(top.values[0] - top.values[1]),
+            "argmax_fp32": int(top32.indices[0]), "margin_fp32": float(top32.values[0] - top32.values[1])}
 
 
 def write_reference(model_dir, result=None, layers=None):

@@ -549,7 +549,7 @@ def test_gemm_swiglu_epilogue_bit_exact(gpu, M, I, K):
     close(act, O.swiglu(g[:, :, 0, :].reshape(M, I), g[:, :, 1, :].reshape(M, I)))
 
 
-@pytest.mark.parametrize("M,N,K,bias,wgs", [(2048, 3584, 18944, False, 224), (1000, 2560, 16384, True, None),
+@pytest.mark.parametrize("M,N,K,bias,wgs", [(2048, 3584, 18944, False, None), (1000, 2560, 16384, True, None),
                                             (2048, 896, 4864, True, None), (2048, 4608, 3584, True, 256),
                                             (2048, 3584, 3584, False, 256)])
 def test_gemm_streamk(gpu, M, N, K, bias, wgs):
@@ -569,14 +569,16 @@ def test_gemm_streamk(gpu, M, N, K, bias, wgs):
 
 
 def test_gemm_streamk_policy(gpu):
-    """The default plan splits K only where the data-parallel tiling fills
-    under 60% of the device and whole pieces of >= 16 K stages fill idle CUs:
-    2048x896x4864 (32 tiles of 76 stages) splits in four; the 7B shapes
-    (down's 256x128 tiles fill 87.5%, q/k/v's 144 tiles leave no room for a
-    second piece), short K (14 stages) and a full-device shape do not."""
+    """The default plan splits K where the data-parallel tiling fills under
+    60% of the device and whole pieces of >= 16 K stages fill idle CUs
+    (2048x896x4864: 32 tiles of 76 stages, four pieces), or under 90% with K
+    of >= 256 stages (the 7B down shape: 256x128 tiles fill 87.5%; two pieces
+    of 148 stages on 112 tiles of 256x256). The other 7B shapes (o: 56
+    stages; q/k/v: 144 tiles leave no room for a second piece), short K (14
+    stages) and a full-device shape do not split."""
     assert ops.gemm_streamk_workspace(2048, 896, 4864) == (32 * 4 * 256 * 256 * 4, 32)
     assert ops.gemm_streamk_workspace(2048, 896, 896) == (0, 0)
-    assert ops.gemm_streamk_workspace(2048, 3584, 18944) == (0, 0)
+    assert ops.gemm_streamk_workspace(2048, 3584, 18944) == (112 * 2 * 256 * 256 * 4, 112)
     assert ops.gemm_streamk_workspace(2048, 3584, 3584) == (0, 0)
     assert ops.gemm_streamk_workspace(2048, 4608, 3584) == (0, 0)
     assert ops.gemm_streamk_workspace(4096, 4096, 18944) == (0, 0)
@@ -608,7 +610,8 @@ def _streamk_case(M, N, K, bias):
 
 
 @pytest.mark.parametrize("M,N,K,k,streamk", [(2048, 3584, 3584, 1, False), (2048, 3584, 3584, 4, False),
-                                             (2048, 3584, 18944, 8, False), (2048, 896, 4864, 4, True),
+                                             (2048, 3584, 18944, 8, False), (2048, 3584, 18944, 4, True),
+                                             (2048, 896, 4864, 4, True),
                                              (2048, 896, 4864, 2, False), (256, 256, 512, 4, False),
                                              (512, 4096, 1024, 2, False), (8192, 4096, 512, 4, False)])
 def test_gemm_add_rmsnorm_relay_bit_exact(gpu, M, N, K, k, streamk):
@@ -616,7 +619,8 @@ def test_gemm_add_rmsnorm_relay_bit_exact(gpu, M, N, K, k, streamk):
     GEMM releases k row tiles and its own workgroups normalise each released
     tile. y, the residual sum and rstd equal the GEMM followed by the
     standalone Add+RMSNorm kernel bit for bit (the 7B o and down shapes, the
-    Qwen2.5-0.5B down shape with its four-piece K split, 64-row tiles); every
+    latter also with its two-piece K split, the Qwen2.5-0.5B down shape with
+    its four-piece K split, 64-row tiles); every
     relay tile's block ends with published == consumed == runs and status 1
     over repeated runs without a host reset; y matches the oracle's
     Add+RMSNorm of the stored product. 8192x4096 with k=4 is a grid of two

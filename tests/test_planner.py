@@ -291,6 +291,38 @@ def test_shipped_mi355x_costs_cover_the_7b_dag():
     assert plan["base_makespan_us"] >= aic
 
 
+@pytest.mark.parametrize("preset", ["qwen2.5-7b", "qwen3-8b"])
+def test_fused_layer_dag(preset):
+    """The DAG of the program the runtime launches: per layer RMSNorm, one
+    QKV projection (RoPE in its epilogue; a q/k RMSNorm and RoPE kernel after
+    it where the model has q/k norms), attention, o, Add+RMSNorm, one gate/up
+    projection (SwiGLU in its epilogue), down, Add+RMSNorm; the same GEMM
+    work as the reference's DAG, without its RoPE, SiLU and Mul passes."""
+    from kernrelay_amd import modeldir
+    cfg = dict(modeldir.PRESETS[preset])
+    H, I, L = cfg["hidden_size"], cfg["intermediate_size"], cfg["num_hidden_layers"]
+    HQ, HKV = cfg["num_attention_heads"], cfg["num_key_value_heads"]
+    D = cfg.get("head_dim") or H // HQ
+    qk = bool(cfg.get("qk_norm", False))
+    ref, dag = P.layer_dag(cfg, 2048), P.layer_dag(cfg, 2048, fused=True)
+    assert len(dag["nodes"]) == 3 + L * (8 + 2 * qk)
+    ops = [n["op"] for n in dag["nodes"]]
+    assert "silu" not in ops and "mul" not in ops and ops.count("rope") == (L if qk else 0)
+    names = {n["name"]: n for n in dag["nodes"]}
+    assert names["l0.qkv"]["shape"] == {"M": 2048, "K": H, "N": (HQ + 2 * HKV) * D}
+    assert names["l0.gate_up"]["shape"] == {"M": 2048, "K": H, "N": 2 * I}
+    assert P.profile_op(names["l0.qkv"]) == "matmul_qkv" and P.profile_op(names["l0.gate_up"]) == "matmul_gate_up"
+    edges = {(e["src"], e["dst"]) for e in dag["edges"]}
+    assert ("l0.gate_up", "l0.down") in edges and ("l0.addnorm1", "l0.gate_up") in edges
+    assert (("l0.rope", "l0.attn") if qk else ("l0.qkv", "l0.attn")) in edges
+    for e in dag["edges"]:
+        assert e["src"] in names and e["dst"] in names
+
+    def flops(d):
+        return sum(2 * n["shape"]["M"] * n["shape"]["K"] * n["shape"]["N"] for n in d["nodes"] if n["op"] == "matmul")
+    assert flops(dag) == flops(ref)
+
+
 def test_relay_edges_taken_only_where_they_pay():
     """An o / down flag edge is kept only where its one relayed launch beats
     the GEMM, the Add+RMSNorm kernel and one more launch; the mode string
