@@ -1098,7 +1098,11 @@ bool PlanStreamK(int M, int N, int K, StreamKPlan &pl)
             const char *e = std::getenv("KR_GEMM_SK_LONGK");
             return e == nullptr || std::atoi(e) != 0;
         }();
-        if (fill >= 0.6 && !(longk && fill < 0.9 && pl.nk >= 256)) return false;
+        static const int longk_nk = [] {
+            const char *e = std::getenv("KR_GEMM_SK_LONGK_NK");
+            return e != nullptr ? std::max(32, std::atoi(e)) : 256;
+        }();
+        if (fill >= 0.6 && !(longk && fill < 0.9 && pl.nk >= longk_nk)) return false;
         const int S = std::min(CuCount() / pl.tiles, pl.nk / 16);
         if (S < 2) return false;
         pl.G = S * pl.tiles;
