@@ -19,7 +19,8 @@
                          file lists (GELU, softmax, cast, add, GEMM at the
                          e3/e9 sizes) on this library's kernels.
 * ``build_costs``      — the cost file: ``full`` = the catalogue shapes plus
-                         every node of the model's planner DAG at its k=1
+                         every node of the model's planner DAG (the
+                         reference's and the fused program's) at its k=1
                          time, ``curves`` = the (k=1, k=8) slope per shape.
 
     python -m kernrelay_amd.profile_model --preset qwen2.5-7b --seq 2048 \\
@@ -174,10 +175,10 @@ def _col(v, k):
 
 def build_costs(cfg, seq, table, consts, dag_full, model=""):
     """The cost file (configs/planner2_costs.json layout plus ``curves``)."""
-    dag = planner.layer_dag(cfg, seq)
+    nodes = planner.layer_dag(cfg, seq)["nodes"] + planner.layer_dag(cfg, seq, fused=True)["nodes"]
     full = dict(dag_full)
     curves = {}
-    for n in dag["nodes"]:
+    for n in nodes:
         v = table.get(planner.profile_op(n)) or {}
         t1, t8 = _col(v, 1), _col(v, 8)
         if not t1:
@@ -230,6 +231,7 @@ def main(argv=None):
         ks = [int(k) for k in args.ks.split(",")]
         t0 = time.time()
         ops = planner.PROFILE_OPS + planner.RELAY_PROFILE_OPS
+        ops += tuple(o for o in planner.FUSED_PROFILE_OPS if o not in ops)
         log("kr_qwen_profile_many %d ops x k=%s" % (len(ops), ks))
         prof = profile(mdir, args.seq, args.device, ks, ops=ops)
         log("profile done in %.1f s" % (time.time() - t0))
