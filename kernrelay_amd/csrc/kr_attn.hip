@@ -418,7 +418,15 @@ AttnKernel(AttnParams p)
             qk(kring[st & 1][hv], sacc);
             mask(sacc, kb * kKvBlk);
             uint4 pf[4];
+            // Two independent 4-wave workgroups share each CU (KH 1): the
+            // wave in its softmax takes issue priority over the other
+            // workgroup's wave on its SIMD (measured at head size 128,
+            // 4096 x 32 heads: 169-176 against 181-187 us p50, 8192 x 32
+            // 612-617 against 616-630; neutral at head size 64 and for the
+            // 8-wave kernel, whose barrier keeps its waves in phase).
+            if constexpr (KH == 1 && D == 128) __builtin_amdgcn_s_setprio(2);
             rescale(softmax(sacc, pf));
+            if constexpr (KH == 1 && D == 128) __builtin_amdgcn_s_setprio(0);
             pv(vring[st & 1][hv], pf);
         }
         KR_WAIT_VM(0);  // this wave's DMA of the next stage has landed
