@@ -412,7 +412,8 @@ def main():
         "serial_tok_s": round(args.steps * S / total_serial_s, 1),
         "split_vs_serial": round(total_serial_s / total_split_s, 4),
         # flag edges kept by the library after replaying every subset in
-        # place (tuned_us: best replay of each), and the planner's choice
+        # place (tuned_us: median replay of each; an edge subset is kept
+        # only if it beats none by more than 0.5%), and the planner's choice
         # from the per-op profile (priced) for comparison
         "relay_edges": {"chosen": head["edges"], "tuned_us": head["tuned_us"], "planned": head["planned_edges"],
                         "priced": head["edge_costs"]},

@@ -214,12 +214,17 @@ def _large_shapes(tmp_path, preset, seq, seed):
         assert b["logits_fnv64"] == a["logits_fnv64"], k
         assert b["flag_timeouts"] == 0 and b["argmax"] == ref["argmax"]
         assert b["relay_edges"] == "o+down" and b["flag_edges"] == 2 * 2 * k
-    # edges chosen in place: every candidate timed, the fastest kept, the same bits
+    # edges chosen in place: every candidate timed (median replay), a flag
+    # edge kept only if it beats the edge-free program by more than 0.5%,
+    # the same bits
     c = run(d, "relay_split:4", seq, iters=1)
     assert c["logits_fnv64"] == a["logits_fnv64"]
     tuned = c["relay_edges_tuned_us"]
     assert set(tuned) == {"none", "o", "down", "o+down"}
-    assert tuned[c["relay_edges"]] == min(tuned.values())
+    if c["relay_edges"] == "none":
+        assert min(tuned.values()) >= tuned["none"] * (1.0 - 0.005)
+    else:
+        assert tuned[c["relay_edges"]] == min(tuned.values()) < tuned["none"] * (1.0 - 0.005)
     return a
 
 
