@@ -64,6 +64,13 @@ def test_oracle_matches_transformers_default_init(dirs, hf_logits, preset):
     err = (got["last_logits"] - ref).abs()
     assert bool((err <= 2e-2 + 1e-2 * ref.abs()).all()), float(err.max())
     assert got["argmax"] == int(ref.argmax())
+    # the unrounded fp32 product of the last row: its top two as transformers'
+    # fp32 logits have them, within the deviation of the stored logits
+    top = torch.topk(ref, 2)
+    if float(top.values[0] - top.values[1]) > 2 * float(err.max()):
+        assert got["argmax_fp32"] == int(top.indices[0])
+    assert got["margin_fp32"] >= 0.0
+    assert abs(got["margin_fp32"] - float(top.values[0] - top.values[1])) <= 2 * float(err.max())
 
 
 @pytest.mark.parametrize("preset", PRESETS)
