@@ -549,12 +549,14 @@ def test_gemm_swiglu_epilogue_bit_exact(gpu, M, I, K):
     close(act, O.swiglu(g[:, :, 0, :].reshape(M, I), g[:, :, 1, :].reshape(M, I)))
 
 
-@pytest.mark.parametrize("M,N,K,bias,wgs", [(2048, 3584, 18944, False, None), (1000, 2560, 16384, True, None),
+@pytest.mark.parametrize("M,N,K,bias,wgs", [(2048, 3584, 18944, False, None), (1920, 3584, 16384, True, None),
+                                            (1000, 2560, 16384, True, None),
                                             (2048, 896, 4864, True, None), (2048, 4608, 3584, True, 256),
                                             (2048, 3584, 3584, False, 256)])
 def test_gemm_streamk(gpu, M, N, K, bias, wgs):
     """Stream-K: the default exact split of K (the down shape: two pieces per
-    tile; a ragged one: four) and, forced over 256 workgroups, the uneven
+    tile; 1920 rows: two pieces on 256x256 tiles whose last row of tiles is
+    half outside M; a ragged one: four) and, forced over 256 workgroups, the uneven
     spread (the q/k/v and o shapes: pieces of unequal length, up to three per
     tile): matches the oracle and the data-parallel kernel within the bf16
     bar, repeats bit for bit (fixed piece order), leaves its counters zero
@@ -579,6 +581,8 @@ def test_gemm_streamk_policy(gpu):
     assert ops.gemm_streamk_workspace(2048, 896, 4864) == (32 * 4 * 256 * 256 * 4, 32)
     assert ops.gemm_streamk_workspace(2048, 896, 896) == (0, 0)
     assert ops.gemm_streamk_workspace(2048, 3584, 18944) == (112 * 2 * 256 * 256 * 4, 112)
+    assert ops.gemm_streamk_workspace(1920, 3584, 16384) == (112 * 2 * 256 * 256 * 4, 112)
+    assert ops.gemm_streamk_workspace(2048, 3584, 16320) == (0, 0)  # 255 stages: below the long-K bar
     assert ops.gemm_streamk_workspace(2048, 3584, 3584) == (0, 0)
     assert ops.gemm_streamk_workspace(2048, 4608, 3584) == (0, 0)
     assert ops.gemm_streamk_workspace(4096, 4096, 18944) == (0, 0)
