@@ -928,8 +928,11 @@ int PipeWaves()
 // 126.7 / 118.5, gate/up 2048x37888x3584 561 / 529, QKV 2048x4608x3584
 // 103 / 85, lm_head 2048x152064x3584 1967 / 1871. Two other schedules
 // measured slower than both: the two waves of a SIMD alternating memory and
-// MFMA phases (4096^3 140 us), and a ring of four or five 32-deep
-// direct-to-LDS stages (142 us: half-line requests). The 4-wave 256x128 and
+// MFMA phases on a direct-to-LDS ring (4096^3 140 us), and a ring of four or
+// five 32-deep direct-to-LDS stages (142 us: half-line requests). The same
+// alternation on the staged refill (per k32 step: fragment reads and half a
+// stage of refill, then 32 MFMAs, a barrier after each phase) gave the same
+// bits in the same time (4096^3 111.0 against 110.1 us). The 4-wave 256x128 and
 // 128x256 kernels keep their three-stage direct-to-LDS ring, which already
 // spreads its refills: staged, they measured 4-8% slower.
 int MainLoopMode()
