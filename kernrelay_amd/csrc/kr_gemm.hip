@@ -384,14 +384,20 @@ __device__ void NormTail(const GemmParams &p, int tile, int worker, int workers)
 // runs would leave every line half-written per instruction). Staged chunk c
 // of a row sits in slot c ^ ((row & 31) >> 1), its 8-byte halves swapped on
 // odd rows. Columns past N are not written.
-template <int DT, int BM, int BN, int NT>
-__device__ __forceinline__ void UnaryTile(const GemmParams &p, const uint16_t *stage, int m0, int n0, bool coh)
+template <int DT, int BM, int BN, int NT, int OP, int ODT>
+__device__ __forceinline__ void UnaryTileOp(const GemmParams &p, const uint16_t *stage, int m0, int n0, bool coh)
 {
-    auto f = [&](uint16_t h) {
+    auto f = [](uint16_t h) {
         const float x = Elem<DT>::Load(h);
-        return p.uop == kEwGelu ? GeluTanh(x) : (p.uop == kEwSilu ? Silu(x) : x);
+        if constexpr (OP == kEwGelu) {
+            return GeluTanh(x);
+        } else if constexpr (OP == kEwSilu) {
+            return Silu(x);
+        } else {
+            return x;
+        }
     };
-    if (p.udt == kF32) {
+    if constexpr (ODT == kF32) {
         constexpr int QPR = BN / 4;  // 4-value quarters per row
 #pragma unroll 4
         for (int idx = threadIdx.x; idx < BM * QPR; idx += NT) {
@@ -413,30 +419,56 @@ __device__ __forceinline__ void UnaryTile(const GemmParams &p, const uint16_t *s
                     if (gn + e < p.N) PutU32(yp + e, __float_as_uint(o[e]), coh);
             }
         }
-        return;
-    }
-    constexpr int CPR = BN / 8;
+    } else {
+        constexpr int CPR = BN / 8;
 #pragma unroll 4
-    for (int idx = threadIdx.x; idx < BM * CPR; idx += NT) {
-        const int row = idx / CPR;
-        const int ch = idx % CPR;
-        const int gm = m0 + row;
-        const int gn = n0 + ch * 8;
-        if (gm >= p.M || gn >= p.N) continue;
-        uint4 u = *reinterpret_cast<const uint4 *>(stage + row * BN + (ch ^ ((row & 31) >> 1)) * 8);
-        if (row & 1) u = make_uint4(u.z, u.w, u.x, u.y);
-        U16x8 a, r;
-        *reinterpret_cast<uint4 *>(a.v) = u;
+        for (int idx = threadIdx.x; idx < BM * CPR; idx += NT) {
+            const int row = idx / CPR;
+            const int ch = idx % CPR;
+            const int gm = m0 + row;
+            const int gn = n0 + ch * 8;
+            if (gm >= p.M || gn >= p.N) continue;
+            uint4 u = *reinterpret_cast<const uint4 *>(stage + row * BN + (ch ^ ((row & 31) >> 1)) * 8);
+            if (row & 1) u = make_uint4(u.z, u.w, u.x, u.y);
+            U16x8 a, r;
+            *reinterpret_cast<uint4 *>(a.v) = u;
 #pragma unroll
-        for (int e = 0; e < 8; ++e) r.v[e] = p.udt == kBF16 ? Elem<kBF16>::Store(f(a.v[e])) : Elem<kF16>::Store(f(a.v[e]));
-        uint16_t *yp = static_cast<uint16_t *>(p.uy) + int64_t(gm) * p.ldy + gn;
-        if (gn + 8 <= p.N) {
-            PutU128(yp, *reinterpret_cast<const uint4 *>(r.v), coh);
-        } else {
+            for (int e = 0; e < 8; ++e) r.v[e] = Elem<ODT>::Store(f(a.v[e]));
+            uint16_t *yp = static_cast<uint16_t *>(p.uy) + int64_t(gm) * p.ldy + gn;
+            if (gn + 8 <= p.N) {
+                PutU128(yp, *reinterpret_cast<const uint4 *>(r.v), coh);
+            } else {
 #pragma unroll
-            for (int e = 0; e < 8; ++e)
-                if (gn + e < p.N) PutU16(yp + e, r.v[e], coh);
+                for (int e = 0; e < 8; ++e)
+                    if (gn + e < p.N) PutU16(yp + e, r.v[e], coh);
+            }
         }
+    }
+}
+
+// The op and output type are the same for the whole launch: one specialised
+// loop each, so no element evaluates another op's or output type's
+// arithmetic (selected at run time inside the loop, both sides were
+// computed for every element).
+template <int DT, int BM, int BN, int NT>
+__device__ __forceinline__ void UnaryTile(const GemmParams &p, const uint16_t *stage, int m0, int n0, bool coh)
+{
+    auto run = [&](auto op) __attribute__((always_inline)) {
+        constexpr int OP = decltype(op)::value;
+        if (p.udt == kF32) {
+            UnaryTileOp<DT, BM, BN, NT, OP, kF32>(p, stage, m0, n0, coh);
+        } else if (p.udt == kBF16) {
+            UnaryTileOp<DT, BM, BN, NT, OP, kBF16>(p, stage, m0, n0, coh);
+        } else {
+            UnaryTileOp<DT, BM, BN, NT, OP, kF16>(p, stage, m0, n0, coh);
+        }
+    };
+    if (p.uop == kEwGelu) {
+        run(std::integral_constant<int, kEwGelu>{});
+    } else if (p.uop == kEwSilu) {
+        run(std::integral_constant<int, kEwSilu>{});
+    } else {
+        run(std::integral_constant<int, kEwCast>{});
     }
 }
 
