@@ -447,9 +447,11 @@ __device__ __forceinline__ void UnaryTileOp(const GemmParams &p, const uint16_t 
 }
 
 // The op and output type are the same for the whole launch: one specialised
-// loop each, so no element evaluates another op's or output type's
-// arithmetic (selected at run time inside the loop, both sides were
-// computed for every element).
+// loop each, dispatched once per tile. Tested at run time inside the
+// element loop, they turned every element into its own small block behind
+// uniform branches, its conversion, exponential and reciprocal chain
+// overlapping no other element's (the mm -> GELU epilogue took 190 instead
+// of 174 us).
 template <int DT, int BM, int BN, int NT>
 __device__ __forceinline__ void UnaryTile(const GemmParams &p, const uint16_t *stage, int m0, int n0, bool coh)
 {
