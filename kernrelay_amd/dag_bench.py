@@ -110,8 +110,12 @@ def tiny(tmp, iters=50, warmup=5):
     dag = workloads.tiny_mm_gelu(tmp)
     serial = _plan(schedule.serial_schedule(dag), tmp, "tiny_serial", iters, warmup)
     split = _plan(workloads.variants(dag, 2)["split"], tmp, "tiny_split2", iters, warmup)
+    # the same split schedule with GELU computed in the GEMM's epilogue
+    reg = _plan(workloads.variants(dag, 2)["split"], tmp, "tiny_split2_epi", iters, warmup,
+                env={"KR_PLAN_EPILOGUE": "1"})
     return {"shape": [256, 512, 512], "serial": _times(serial), "split2": _times(split),
-            "checksums_equal": serial["checksum"] == split["checksum"]}
+            "split2_register_relay": dict(_times(reg), epilogue_consumers=reg.get("epilogue_consumers")),
+            "checksums_equal": serial["checksum"] == split["checksum"] == reg["checksum"]}
 
 
 # The reference's relay table (Ascend 910B3, nhp_exec, best of 3 x 5 runs):
